@@ -1,0 +1,29 @@
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "api_common.hpp"
+
+namespace c4q {
+
+static thread_local char g_err[512] = "";
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+}
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("%s: kernel launch failed: %s", what, hipGetErrorString(e));
+    return C4Q_ERR_HIP;
+  }
+  return C4Q_OK;
+}
+
+}  // namespace c4q
+
+extern "C" const char* c4q_last_error(void) { return c4q::g_err; }
+extern "C" int c4q_abi_version(void) { return C4Q_ABI_VERSION; }

@@ -1,0 +1,94 @@
+// FP8 e4m3fn x e4m3fn scaled GEMM (torch._scaled_mm semantics) and the
+// W8A16 (bf16/f16 activation x fp8 weight) linear.
+#include "launch.hpp"
+
+using namespace c4q;
+
+namespace {
+
+bool valid_dt(int dt) { return dt == C4Q_BF16 || dt == C4Q_F16 || dt == C4Q_F32; }
+bool valid_mode(int m) { return m == C4Q_SCALE_NONE || m == C4Q_SCALE_TENSOR || m == C4Q_SCALE_VECTOR; }
+
+template <bool BF16, bool HAS_SCALE, class Epi>
+int run_w8a16_tiled(const uint16_t* a, int64_t lda, const uint8_t* w, int64_t ldw,
+                    const float* w_scale, int64_t M, int64_t N, int64_t K, const Epi& epi,
+                    hipStream_t s, const char* what) {
+  using Mma = typename std::conditional<BF16, MmaBF16, MmaF16>::type;
+  GemmShape sh{M, N, K, 2 * K, K, 0, 0};
+  RowsPlain ra{reinterpret_cast<const uint8_t*>(a), 2 * lda, M};
+  RowsPlain rb{w, ldw, N};
+  BStoreDequant<BF16> bst{w_scale, 1.0f};
+  switch (pick_tile(M, N)) {
+    case TILE_256x256:
+      return launch_tile<Mma, 256, 256, Load8<256, RowsPlain>, RowsPlain,
+                         LoadW8<256, BF16, HAS_SCALE>, RowsPlain, BStoreDequant<BF16>, false>(
+          sh, N, ra, rb, bst, epi, s, what);
+    case TILE_128x128:
+      return launch_tile<Mma, 128, 128, Load8<128, RowsPlain>, RowsPlain,
+                         LoadW8<128, BF16, HAS_SCALE>, RowsPlain, BStoreDequant<BF16>, false>(
+          sh, N, ra, rb, bst, epi, s, what);
+    default:
+      return launch_tile<Mma, 64, 128, Load8<64, RowsPlain>, RowsPlain,
+                         LoadW8<128, BF16, HAS_SCALE>, RowsPlain, BStoreDequant<BF16>, false>(
+          sh, N, ra, rb, bst, epi, s, what);
+  }
+}
+
+}  // namespace
+
+extern "C" int c4q_f8_gemm_nt_scaled(const uint8_t* a, int64_t lda, const uint8_t* b, int64_t ldb,
+                                     void* d, int d_dtype, int64_t ldd, const float* scale_a,
+                                     int scale_a_mode, const float* scale_b, int scale_b_mode,
+                                     const float* scale_result, const void* bias, int bias_dtype,
+                                     int64_t M, int64_t N, int64_t K, void* stream) {
+  const char* what = "c4q_f8_gemm_nt_scaled";
+  C4Q_REQUIRE(M >= 0 && N >= 0 && K >= 0, C4Q_ERR_SHAPE, "%s: negative size", what);
+  C4Q_REQUIRE(lda >= K && ldb >= K && ldd >= N, C4Q_ERR_SHAPE, "%s: row stride smaller than row",
+              what);
+  C4Q_REQUIRE(valid_dt(d_dtype), C4Q_ERR_ARG, "%s: bad output dtype %d", what, d_dtype);
+  C4Q_REQUIRE(valid_mode(scale_a_mode) && valid_mode(scale_b_mode), C4Q_ERR_ARG,
+              "%s: bad scale mode", what);
+  C4Q_REQUIRE(scale_a_mode == C4Q_SCALE_NONE || scale_a, C4Q_ERR_ARG, "%s: null scale_a", what);
+  C4Q_REQUIRE(scale_b_mode == C4Q_SCALE_NONE || scale_b, C4Q_ERR_ARG, "%s: null scale_b", what);
+  C4Q_REQUIRE(!bias || valid_dt(bias_dtype), C4Q_ERR_ARG, "%s: bad bias dtype", what);
+  if (M == 0 || N == 0) return C4Q_OK;
+  C4Q_REQUIRE(d && (K == 0 || (a && b)), C4Q_ERR_ARG, "%s: null pointer", what);
+  EpiScaled epi{d, ldd, d_dtype, scale_a, scale_a_mode, scale_b, scale_b_mode, scale_result,
+                bias, bias_dtype, 1.0f, 1.0f, 1.0f};
+  return run_gemm8<MmaF8, GenF8>(a, lda, b, ldb, M, N, K, epi, as_stream(stream), what);
+}
+
+extern "C" int c4q_w8a16_gemm_nt(const void* a, int a_dtype, int64_t lda, const uint8_t* w,
+                                 int64_t ldw, const float* w_scale, void* d, int d_dtype,
+                                 int64_t ldd, const void* bias, int bias_dtype,
+                                 const uint16_t* act_table, int64_t M, int64_t N, int64_t K,
+                                 void* stream) {
+  const char* what = "c4q_w8a16_gemm_nt";
+  C4Q_REQUIRE(M >= 0 && N >= 0 && K >= 0, C4Q_ERR_SHAPE, "%s: negative size", what);
+  C4Q_REQUIRE(lda >= K && ldw >= K && ldd >= N, C4Q_ERR_SHAPE, "%s: row stride smaller than row",
+              what);
+  C4Q_REQUIRE(a_dtype == C4Q_BF16 || a_dtype == C4Q_F16, C4Q_ERR_ARG,
+              "%s: activation must be bf16 or f16", what);
+  C4Q_REQUIRE(valid_dt(d_dtype), C4Q_ERR_ARG, "%s: bad output dtype %d", what, d_dtype);
+  C4Q_REQUIRE(!bias || valid_dt(bias_dtype), C4Q_ERR_ARG, "%s: bad bias dtype", what);
+  C4Q_REQUIRE(!act_table || d_dtype == C4Q_BF16, C4Q_ERR_UNSUPPORTED,
+              "%s: act_table needs a bf16 output", what);
+  if (M == 0 || N == 0) return C4Q_OK;
+  C4Q_REQUIRE(d && (K == 0 || (a && w)), C4Q_ERR_ARG, "%s: null pointer", what);
+  hipStream_t s = as_stream(stream);
+  EpiW8A16 epi{d, ldd, d_dtype, bias, bias_dtype, act_table};
+  const bool bf16 = a_dtype == C4Q_BF16;
+  const bool tiled = K > 0 && K % 16 == 0 && aligned16(a) && aligned16(w) && lda % 8 == 0 &&
+                     ldw % 16 == 0;
+  if (!tiled) {
+    GenW8A16 op{static_cast<const uint16_t*>(a), lda, w, ldw, w_scale, bf16 ? 1 : 0, 1.0f};
+    return launch_generic(M, N, K, op, epi, s, what);
+  }
+  const uint16_t* a16 = static_cast<const uint16_t*>(a);
+  if (bf16) {
+    return w_scale ? run_w8a16_tiled<true, true>(a16, lda, w, ldw, w_scale, M, N, K, epi, s, what)
+                   : run_w8a16_tiled<true, false>(a16, lda, w, ldw, w_scale, M, N, K, epi, s, what);
+  }
+  return w_scale ? run_w8a16_tiled<false, true>(a16, lda, w, ldw, w_scale, M, N, K, epi, s, what)
+                 : run_w8a16_tiled<false, false>(a16, lda, w, ldw, w_scale, M, N, K, epi, s, what);
+}

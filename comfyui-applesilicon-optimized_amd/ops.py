@@ -1,0 +1,411 @@
+"""Tensor-level entry points over libcdna4q.so.
+
+Names, argument meaning and error behaviour follow the reference's native
+modules (pybind11 functions taking tensors; a bad argument raises
+RuntimeError before any work is enqueued):
+
+    i8_matmul2d_nt, i8_matmul2d_nt_fused, i8_matmul2d_nt_fused_cs,
+    i8_quant_rowwise                 (_patches/int8_ext/int8_gemm.mm:2626-2715)
+    fp8fp8_matmul2d_nt               (_patches/fp8_ext/fp8_matmul2d.mm:229-265)
+    w8a16_f32, w8a16_bias_bf16       (_patches/fp8s_ext/w8a16_gemm.mm:286-329)
+
+plus the whole-operation forms the patch layer uses: ``int_mm``
+(torch._int_mm), ``scaled_mm`` (torch._scaled_mm), ``fp8_quant_pertensor``,
+``fp8_dequant``, ``w8a16_linear`` and ``ffn_pair``.
+
+Every function enqueues on the current HIP stream of the tensors' device and
+returns without synchronizing. Outputs are allocated here with torch; the
+library itself never allocates.
+"""
+import torch
+import torch.nn.functional as F
+
+from . import _lib
+from ._lib import BF16, F16, F32, SCALE_NONE, SCALE_TENSOR, SCALE_VECTOR, C4QError
+
+_FLOAT_CODE = {torch.bfloat16: BF16, torch.float16: F16, torch.float32: F32}
+FP8 = torch.float8_e4m3fn
+
+
+def _req(cond, msg):
+    if not cond:
+        raise C4QError(msg)
+
+
+def _dev(*tensors):
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        _req(t.device.type == "cuda", f"tensor on {t.device}, expected a ROCm (cuda) device")
+        if dev is None:
+            dev = t.device
+        _req(t.device == dev, f"tensors on different devices ({dev} vs {t.device})")
+    return dev
+
+
+def _ld(t, name):
+    """Row stride (elements) of a 2-D tensor whose rows are contiguous."""
+    _req(t.dim() == 2, f"{name} must be 2D")
+    _req(t.size(1) <= 1 or t.stride(1) == 1, f"{name} rows must be contiguous")
+    if t.size(0) <= 1:
+        return max(t.size(1), 1)
+    _req(t.stride(0) >= t.size(1), f"{name} has overlapping rows")
+    return t.stride(0)
+
+
+def _vec(t, n, dtype, name):
+    _req(t.dtype == dtype, f"{name} must be {dtype}")
+    _req(t.numel() == n and t.is_contiguous(), f"{name} must be contiguous with {n} elements")
+    return t
+
+
+def _stream(dev):
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+class _on(object):
+    """Make `dev` the current device for the duration of a launch."""
+
+    def __init__(self, dev):
+        self.dev = dev
+        self.ctx = None
+
+    def __enter__(self):
+        if self.dev.index is not None and self.dev.index != torch.cuda.current_device():
+            self.ctx = torch.cuda.device(self.dev)
+            self.ctx.__enter__()
+
+    def __exit__(self, *exc):
+        if self.ctx is not None:
+            self.ctx.__exit__(*exc)
+
+
+# ------------------------------------------------------------------ INT8 ---
+
+def _i8_operands(a, b):
+    _req(a.dtype == torch.int8 and b.dtype == torch.int8, "a/b must be int8")
+    _req(a.dim() == 2 and b.dim() == 2, "a/b must be 2D")
+    _req(a.size(1) == b.size(1), "K mismatch: A[M,K], B[N,K]")
+    return _dev(a, b), _ld(a, "a"), _ld(b, "b")
+
+
+def i8_matmul2d_nt(a_i8, b_i8):
+    """C[M,N] int32 = A[M,K] int8 @ B[N,K]^T int8, exact."""
+    dev, lda, ldb = _i8_operands(a_i8, b_i8)
+    M, K = a_i8.shape
+    N = b_i8.size(0)
+    c = torch.empty((M, N), dtype=torch.int32, device=dev)
+    with _on(dev):
+        _lib.call("c4q_i8_gemm_nt_i32", a_i8.data_ptr(), lda, b_i8.data_ptr(), ldb,
+                  c.data_ptr(), N, M, N, K, _stream(dev))
+    return c
+
+
+def int_mm(a, b):
+    """``torch._int_mm(a, b)``: a [M,K] int8 @ b [K,N] int8 -> int32.
+    ``b`` is usually ``weight.T`` of an [N,K] weight, whose transpose is the
+    NT kernel's operand as-is (reference _patches/int_mm_mps.py:98-103)."""
+    _req(a.dim() == 2 and b.dim() == 2 and a.size(1) == b.size(0), "int_mm: a[M,K] @ b[K,N]")
+    bt = b.t()
+    if bt.size(1) > 1 and bt.stride(1) != 1:
+        bt = bt.contiguous()
+    if a.size(1) > 1 and a.stride(1) != 1:
+        a = a.contiguous()
+    return i8_matmul2d_nt(a, bt)
+
+
+def _bias_bf16(bias, n):
+    if bias is None:
+        return None
+    return _vec(bias.to(torch.bfloat16).contiguous().reshape(-1), n, torch.bfloat16, "bias")
+
+
+def i8_matmul2d_nt_fused(a_i8, b_i8, row_scale, bias=None):
+    """D[M,N] bf16 = bf16(f32(A@B^T) * row_scale[m]) [+ bf16 bias]."""
+    dev, lda, ldb = _i8_operands(a_i8, b_i8)
+    M, K = a_i8.shape
+    N = b_i8.size(0)
+    _dev(row_scale, bias)
+    _vec(row_scale, M, torch.float32, "row_scale")
+    bias = _bias_bf16(bias, N)
+    d = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    with _on(dev):
+        _lib.call("c4q_i8_gemm_nt_fused", a_i8.data_ptr(), lda, b_i8.data_ptr(), ldb,
+                  d.data_ptr(), N, row_scale.data_ptr(),
+                  bias.data_ptr() if bias is not None else None, M, N, K, _stream(dev))
+    return d
+
+
+def i8_matmul2d_nt_fused_cs(a_i8, b_i8, row_scale, col_scale, bias=None, split_tail=False,
+                            long_schedule=True, moss_schedule=False):
+    """D[M,N] bf16 = bf16(f32(A@B^T) * (col_scale[n] * row_scale[m])) [+ bias].
+    The reference's schedule switches select tile orders that change no
+    output byte; they are accepted and have no effect here."""
+    del split_tail, long_schedule, moss_schedule
+    dev, lda, ldb = _i8_operands(a_i8, b_i8)
+    M, K = a_i8.shape
+    N = b_i8.size(0)
+    _dev(row_scale, col_scale, bias)
+    _vec(row_scale, M, torch.float32, "row_scale")
+    _vec(col_scale, N, torch.float32, "col_scale")
+    bias = _bias_bf16(bias, N)
+    d = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    with _on(dev):
+        _lib.call("c4q_i8_gemm_nt_fused_cs", a_i8.data_ptr(), lda, b_i8.data_ptr(), ldb,
+                  d.data_ptr(), N, row_scale.data_ptr(), col_scale.data_ptr(),
+                  bias.data_ptr() if bias is not None else None, M, N, K, _stream(dev))
+    return d
+
+
+def i8_quant_rowwise(x):
+    """x[M,K] bf16/f16 -> (q[M,K] int8, scales[M,1] fp32), bit-exact with
+    comfy_kitchen quantize_int8_rowwise."""
+    _req(x.dim() == 2, "x must be 2D [M,K]")
+    _req(x.dtype in (torch.bfloat16, torch.float16), "x must be bf16 or f16")
+    dev = _dev(x)
+    ldx = _ld(x, "x")
+    M, K = x.shape
+    q = torch.empty((M, K), dtype=torch.int8, device=dev)
+    scales = torch.empty((M, 1), dtype=torch.float32, device=dev)
+    with _on(dev):
+        _lib.call("c4q_i8_quant_rowwise", x.data_ptr(), _FLOAT_CODE[x.dtype], ldx, q.data_ptr(),
+                  max(K, 1), scales.data_ptr(), M, K, _stream(dev))
+    return q, scales
+
+
+def ffn_pair(q, w_gate, w_up, row_scale, gate_scale, up_scale, table_gate=None, table_up=None):
+    """Fused gate/up pair, bf16 [M, N_out]:
+    bf16(f32(T1[g]) * f32(T2[u])) with g, u the per-channel fused bf16
+    projections; a None table is the identity."""
+    _req(w_gate.shape == w_up.shape, "gate/up weights differ in shape")
+    dev, lda, ldw = _i8_operands(q, w_gate)
+    _req(_ld(w_up, "w_up") == ldw, "gate/up weights must share a row stride")
+    _dev(w_up, row_scale, gate_scale, up_scale, table_gate, table_up)
+    M, K = q.shape
+    N = w_gate.size(0)
+    _vec(row_scale.reshape(-1), M, torch.float32, "row_scale")
+    _vec(gate_scale.reshape(-1), N, torch.float32, "gate_scale")
+    _vec(up_scale.reshape(-1), N, torch.float32, "up_scale")
+    for t in (table_gate, table_up):
+        if t is not None:
+            _req(t.numel() == 65536 and t.element_size() == 2 and t.is_contiguous(),
+                 "activation tables must be 65536 contiguous 16-bit entries")
+    d = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    with _on(dev):
+        _lib.call("c4q_i8_ffn_pair", q.data_ptr(), lda, w_gate.data_ptr(), w_up.data_ptr(), ldw,
+                  d.data_ptr(), N, row_scale.data_ptr(), gate_scale.data_ptr(),
+                  up_scale.data_ptr(),
+                  table_gate.data_ptr() if table_gate is not None else None,
+                  table_up.data_ptr() if table_up is not None else None, M, N, K, _stream(dev))
+    return d
+
+
+# ------------------------------------------------------------------- FP8 ---
+
+def _as_u8(t):
+    return t.view(torch.uint8) if t.dtype == FP8 else t
+
+
+def _scale_mode(s, n, name):
+    if s is None:
+        return SCALE_NONE, None
+    s = s.to(torch.float32).contiguous()
+    if s.numel() == 1:
+        return SCALE_TENSOR, s
+    _req(s.numel() == n, f"{name} must have 1 or {n} elements")
+    return SCALE_VECTOR, s
+
+
+def _f8_gemm(a_u8, lda, w_u8, ldw, M, N, K, dev, out_dtype, scale_a=None, scale_b=None,
+             scale_result=None, bias=None):
+    _req(out_dtype in _FLOAT_CODE, f"unsupported out_dtype {out_dtype}")
+    am, sa = _scale_mode(scale_a, M, "scale_a")
+    bm, sb = _scale_mode(scale_b, N, "scale_b")
+    sr = None
+    if scale_result is not None:
+        sr = scale_result.to(torch.float32).contiguous()
+        _req(sr.numel() == 1, "scale_result must be a scalar tensor")
+    bdt = F32
+    if bias is not None:
+        _req(bias.dtype in _FLOAT_CODE, "bias must be bf16, f16 or f32")
+        bias = bias.contiguous().reshape(-1)
+        _req(bias.numel() == N, f"bias must have {N} elements")
+        bdt = _FLOAT_CODE[bias.dtype]
+    _dev(sa, sb, sr, bias)
+    d = torch.empty((M, N), dtype=out_dtype, device=dev)
+    with _on(dev):
+        _lib.call("c4q_f8_gemm_nt_scaled", a_u8.data_ptr(), lda, w_u8.data_ptr(), ldw,
+                  d.data_ptr(), _FLOAT_CODE[out_dtype], N,
+                  sa.data_ptr() if sa is not None else None, am,
+                  sb.data_ptr() if sb is not None else None, bm,
+                  sr.data_ptr() if sr is not None else None,
+                  bias.data_ptr() if bias is not None else None, bdt, M, N, K, _stream(dev))
+    return d
+
+
+def fp8fp8_matmul2d_nt(a_u8, w_u8, K=None, N=None):
+    """C[M,N] f32 (unscaled) = A[M,K] fp8 @ W[N,K]^T fp8 (e4m3fn bytes)."""
+    a_u8, w_u8 = _as_u8(a_u8), _as_u8(w_u8)
+    _req(a_u8.dtype == torch.uint8 and w_u8.dtype == torch.uint8, "a/w must be fp8 bytes")
+    _req(a_u8.dim() == 2 and w_u8.dim() == 2 and a_u8.size(1) == w_u8.size(1),
+         "K mismatch: A[M,K], W[N,K]")
+    _req(K is None or K == a_u8.size(1), "K does not match the operands")
+    _req(N is None or N == w_u8.size(0), "N does not match the weight")
+    dev = _dev(a_u8, w_u8)
+    M, K = a_u8.shape
+    return _f8_gemm(a_u8, _ld(a_u8, "a"), w_u8, _ld(w_u8, "w"), M, w_u8.size(0), K, dev,
+                    torch.float32)
+
+
+def scaled_mm(input, other, *, out_dtype=None, scale_a=None, scale_b=None, bias=None,
+              scale_result=None, use_fast_accum=False):
+    """``torch._scaled_mm`` for e4m3fn operands on the fp8 route:
+    out = f32(input @ other); *= scale_a; *= scale_b; *= scale_result;
+    += f32(bias); -> out_dtype (f32 when None). Per-tensor or vector scales
+    (scale_a [M,1] rowwise, scale_b [1,N] columnwise). Accumulation is fp32
+    regardless of use_fast_accum."""
+    del use_fast_accum
+    _req(input.dtype == FP8 and other.dtype == FP8, "scaled_mm: operands must be float8_e4m3fn")
+    _req(input.dim() == 2 and other.dim() == 2 and input.size(1) == other.size(0),
+         "scaled_mm: input[M,K] @ other[K,N]")
+    dev = _dev(input, other)
+    a = input if (input.size(1) <= 1 or input.stride(1) == 1) else input.contiguous()
+    w = other.t()
+    if w.size(1) > 1 and w.stride(1) != 1:
+        w = w.contiguous()
+    M, K = a.shape
+    N = w.size(0)
+    return _f8_gemm(a.view(torch.uint8), _ld(a, "input"), w.view(torch.uint8), _ld(w, "other^T"),
+                    M, N, K, dev, out_dtype if out_dtype is not None else torch.float32,
+                    scale_a, scale_b, scale_result, bias)
+
+
+def fp8_quant_pertensor(x):
+    """Dynamic per-tensor e4m3fn quant: (q same shape as x, scale [] fp32)."""
+    _req(x.dtype in (torch.bfloat16, torch.float16), "x must be bf16 or f16")
+    dev = _dev(x)
+    x = x.contiguous()
+    q = torch.empty(x.shape, dtype=FP8, device=dev)
+    ws = torch.empty(2, dtype=torch.float32, device=dev)
+    with _on(dev):
+        _lib.call("c4q_f8_quant_pertensor", x.data_ptr(), _FLOAT_CODE[x.dtype], x.numel(),
+                  q.data_ptr(), ws.data_ptr(), ws.data_ptr() + 4, _stream(dev))
+    return q, ws[0]
+
+
+def fp8_dequant(w, scale=None, out_dtype=torch.bfloat16):
+    """comfy_kitchen dequantize_per_tensor_fp8: out_dtype(w) * out_dtype(scale),
+    one rounding of the product; plain exact decode when scale is None."""
+    _req(w.dtype in (FP8, torch.uint8), "w must be float8_e4m3fn")
+    _req(out_dtype in _FLOAT_CODE, "out_dtype must be bf16, f16 or f32")
+    dev = _dev(w, scale)
+    w = w.contiguous()
+    if scale is not None:
+        scale = scale.to(torch.float32).contiguous()
+        _req(scale.numel() == 1, "per-tensor scale must be a scalar")
+    out = torch.empty(w.shape, dtype=out_dtype, device=dev)
+    with _on(dev):
+        _lib.call("c4q_fp8_dequant", w.data_ptr(), w.numel(),
+                  scale.data_ptr() if scale is not None else None, out.data_ptr(),
+                  _FLOAT_CODE[out_dtype], _stream(dev))
+    return out
+
+
+def w8a16_linear(x, weight, w_scale=None, bias=None, out_dtype=None, act_table=None):
+    """W8A16 linear over the last dim of x (bf16/f16): the fp8 [N,K] weight
+    is dequantized in registers to x's dtype (kitchen formula when w_scale is
+    given), fp32 accumulate, out = out_dtype(acc + f32 bias) rounded once,
+    then the optional 65,536-entry bf16 activation table."""
+    _req(x.dtype in (torch.bfloat16, torch.float16), "x must be bf16 or f16")
+    _req(weight.dtype in (FP8, torch.uint8) and weight.dim() == 2, "weight must be fp8 [N,K]")
+    _req(x.size(-1) == weight.size(1), "K mismatch")
+    out_dtype = out_dtype or x.dtype
+    _req(out_dtype in _FLOAT_CODE, "out_dtype must be bf16, f16 or f32")
+    dev = _dev(x, weight, w_scale, bias, act_table)
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, x.size(-1))
+    if x2.size(1) > 1 and x2.stride(1) != 1:
+        x2 = x2.contiguous()
+    w = weight.view(torch.uint8) if weight.dtype == FP8 else weight
+    M, K = x2.shape
+    N = w.size(0)
+    if w_scale is not None:
+        w_scale = w_scale.to(torch.float32).contiguous()
+        _req(w_scale.numel() == 1, "w_scale must be a per-tensor scalar")
+    bdt = F32
+    if bias is not None:
+        _req(bias.dtype in _FLOAT_CODE, "bias must be bf16, f16 or f32")
+        bias = bias.contiguous().reshape(-1)
+        _req(bias.numel() == N, f"bias must have {N} elements")
+        bdt = _FLOAT_CODE[bias.dtype]
+    if act_table is not None:
+        _req(out_dtype == torch.bfloat16, "act_table needs a bf16 output")
+        _req(act_table.numel() == 65536 and act_table.element_size() == 2
+             and act_table.is_contiguous(), "act_table must be 65536 contiguous 16-bit entries")
+    d = torch.empty((M, N), dtype=out_dtype, device=dev)
+    with _on(dev):
+        _lib.call("c4q_w8a16_gemm_nt", x2.data_ptr(), _FLOAT_CODE[x2.dtype], _ld(x2, "x"),
+                  w.data_ptr(), _ld(w, "weight"),
+                  w_scale.data_ptr() if w_scale is not None else None,
+                  d.data_ptr(), _FLOAT_CODE[out_dtype], N,
+                  bias.data_ptr() if bias is not None else None, bdt,
+                  act_table.data_ptr() if act_table is not None else None, M, N, K, _stream(dev))
+    return d.reshape(*lead, N)
+
+
+def w8a16_f32(a, w_u8, variant=-1):
+    """C[M,N] f32 = A[M,K] (f16/bf16) @ W[N,K]^T fp8. ``variant`` picked the
+    reference's Metal tile geometry; tiles are chosen by shape here."""
+    del variant
+    _req(a.dim() == 2, "a must be 2D")
+    return w8a16_linear(a, w_u8, out_dtype=torch.float32)
+
+
+def w8a16_bias_bf16(a, w_u8, bias=None, variant=-1):
+    """D[M,N] bf16 = bf16(A @ W^T + f32 bias[n]) (fused epilogue)."""
+    del variant
+    _req(a.dim() == 2, "a must be 2D")
+    if bias is not None:
+        _req(bias.dtype == torch.float32, "bias must be f32")
+    return w8a16_linear(a, w_u8, bias=bias, out_dtype=torch.bfloat16)
+
+
+# ------------------------------------------------------ activation tables ---
+
+_TABLES = {}
+
+
+def act_table(name, device):
+    """65,536-entry bf16 table of activation `name` ('silu' | 'gelu_tanh')
+    built once per device with torch's own op on that device, so a fused
+    epilogue reproduces the unfused "bf16 tensor -> F.<act>" chain there."""
+    device = torch.device(device)
+    key = (name, device)
+    t = _TABLES.get(key)
+    if t is None:
+        v = torch.arange(65536, dtype=torch.int32, device=device).to(torch.int16).view(torch.bfloat16)
+        if name == "silu":
+            r = F.silu(v)
+        elif name == "gelu_tanh":
+            r = F.gelu(v, approximate="tanh")
+        else:
+            raise C4QError(f"unknown activation {name!r}")
+        t = r.contiguous().view(torch.int16)
+        _TABLES[key] = t
+    return t
+
+
+def situ_tables(device):
+    """MOSS SiTU tables T_h = 25 tanh(v/25), T_g = 4 tanh(v/4) sigmoid(v) over
+    every bf16 v, each op in bf16 (reference _patches/moss_fast.py:97-99)."""
+    device = torch.device(device)
+    key = ("situ", device)
+    t = _TABLES.get(key)
+    if t is None:
+        v = torch.arange(65536, dtype=torch.int32, device=device).to(torch.int16).view(torch.bfloat16)
+        th = (25.0 * torch.tanh(v / 25.0)).contiguous().view(torch.int16)
+        tg = (4.0 * torch.tanh(v / 4.0) * torch.sigmoid(v)).contiguous().view(torch.int16)
+        t = (th, tg)
+        _TABLES[key] = t
+    return t

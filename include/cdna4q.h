@@ -1,0 +1,146 @@
+/*
+ * cdna4q — quantized linear kernels for AMD Instinct MI355X (gfx950).
+ *
+ * Plain C ABI over HIP. Every entry point:
+ *   - takes device pointers, element strides ("ld" = distance between rows,
+ *     in elements) and sizes; tensors are row-major, K is the contiguous
+ *     (reduction) dimension of both GEMM operands ("NT": D = A @ B^T with B
+ *     stored [N, K], the nn.Linear weight layout);
+ *   - enqueues asynchronously on `stream` (a hipStream_t; NULL = the null
+ *     stream) and never synchronizes, allocates device memory or frees it;
+ *     all buffers belong to the caller;
+ *   - returns C4Q_OK (0) or a negative status; c4q_last_error() then holds a
+ *     message (thread-local). Invalid arguments are rejected before anything
+ *     is enqueued.
+ *
+ * Layout contract of the fast (MFMA-tiled) kernels: base pointers 16-byte
+ * aligned, row strides a multiple of 16 bytes, K a multiple of 16. Calls
+ * outside it are still computed, bit-identically where the result is
+ * integer/byte exact, by shape-agnostic fallback kernels.
+ *
+ * Each declaration names the reference (luix93/ComfyUI-AppleSilicon-Optimized)
+ * interface it replaces, as path:line under that repository.
+ */
+#ifndef CDNA4Q_H
+#define CDNA4Q_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define C4Q_ABI_VERSION 1
+
+/* status codes */
+#define C4Q_OK 0
+#define C4Q_ERR_ARG (-1)          /* null pointer, bad enum value          */
+#define C4Q_ERR_SHAPE (-2)        /* negative size, stride smaller than row */
+#define C4Q_ERR_HIP (-4)          /* HIP launch / runtime error             */
+#define C4Q_ERR_UNSUPPORTED (-5)  /* valid but unsupported combination      */
+
+/* element types of floating-point tensors */
+#define C4Q_BF16 0
+#define C4Q_F16 1
+#define C4Q_F32 2
+
+/* scale layouts of c4q_f8_gemm_nt_scaled */
+#define C4Q_SCALE_NONE 0
+#define C4Q_SCALE_TENSOR 1   /* one fp32 value                         */
+#define C4Q_SCALE_VECTOR 2   /* scale_a: [M] (rows); scale_b: [N] (cols) */
+
+const char* c4q_last_error(void);
+int c4q_abi_version(void);
+
+/* C[M,N] int32 = A[M,K] int8 @ B[N,K]^T int8, exact.
+ * Replaces i8_matmul2d_nt (_patches/int8_ext/int8_gemm.mm:1655-1703), the
+ * kernel behind the torch._int_mm seam (_patches/int_mm_mps.py:90-110). */
+int c4q_i8_gemm_nt_i32(const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb,
+                       int32_t* c, int64_t ldc, int64_t M, int64_t N, int64_t K,
+                       void* stream);
+
+/* D[M,N] bf16 = bf16(f32(A@B^T) * row_scale[m]) [then bf16(D + bias[n])].
+ * row_scale: fp32 [M]; bias: bf16 [N] or NULL.
+ * Replaces i8_matmul2d_nt_fused (_patches/int8_ext/int8_gemm.mm:1709-1774). */
+int c4q_i8_gemm_nt_fused(const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb,
+                         uint16_t* d, int64_t ldd, const float* row_scale,
+                         const uint16_t* bias, int64_t M, int64_t N, int64_t K,
+                         void* stream);
+
+/* D[M,N] bf16 = bf16(f32(A@B^T) * (col_scale[n] * row_scale[m])) [+ bias].
+ * Replaces i8_matmul2d_nt_fused_cs (_patches/int8_ext/int8_gemm.mm:1823-1954);
+ * its schedule switches (split_tail, long_schedule, moss_schedule) change no
+ * output byte and have no counterpart here. */
+int c4q_i8_gemm_nt_fused_cs(const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb,
+                            uint16_t* d, int64_t ldd, const float* row_scale,
+                            const float* col_scale, const uint16_t* bias,
+                            int64_t M, int64_t N, int64_t K, void* stream);
+
+/* Rowwise int8 activation quant of x[M,K] (bf16 or f16):
+ * q[M,K] int8 and scales[M] fp32, bit-exact with comfy_kitchen
+ * quantize_int8_rowwise. Replaces i8_quant_rowwise
+ * (_patches/int8_ext/int8_gemm.mm:2332-2373, arithmetic :1337-1381). */
+int c4q_i8_quant_rowwise(const void* x, int x_dtype, int64_t ldx, int8_t* q, int64_t ldq,
+                         float* scales, int64_t M, int64_t K, void* stream);
+
+/* torch._scaled_mm fp8 route: D[M,N] = out_dtype(((f32(A@B^T) * scale_a)
+ * * scale_b) * scale_result + f32(bias[n])). A [M,K] and B [N,K] are e4m3fn
+ * bytes; scale_result and bias may be NULL.
+ * Replaces fp8fp8_matmul2d_nt (_patches/fp8_ext/fp8_matmul2d.mm:229-265)
+ * together with the fp32 scale/bias tail of _fast_route
+ * (_patches/scaled_mm_fp8.py:123-146). */
+int c4q_f8_gemm_nt_scaled(const uint8_t* a, int64_t lda, const uint8_t* b, int64_t ldb,
+                          void* d, int d_dtype, int64_t ldd,
+                          const float* scale_a, int scale_a_mode,
+                          const float* scale_b, int scale_b_mode,
+                          const float* scale_result, const void* bias, int bias_dtype,
+                          int64_t M, int64_t N, int64_t K, void* stream);
+
+/* Dynamic per-tensor e4m3fn quant of n contiguous elements (bf16/f16):
+ * scale[0] = amax/448 (1 if the tensor is all zeros), q = e4m3fn(clamp(x /
+ * scale, +-448)). amax_ws: one fp32 of caller scratch.
+ * The caller side of torch._scaled_mm; the clamp-then-cast follows
+ * comfy_kitchen quantize_per_tensor_fp8 (_patches/comfykitchen_fp8.py:91-97). */
+int c4q_f8_quant_pertensor(const void* x, int x_dtype, int64_t n, uint8_t* q,
+                           float* scale, float* amax_ws, void* stream);
+
+/* out[n] = T(decode(w[n]) * T(scale[0])) for T = out_dtype (bf16/f16); the
+ * plain exact decode when scale is NULL. Replaces comfy_kitchen
+ * dequantize_per_tensor_fp8 (_patches/comfykitchen_fp8.py:86-89) and
+ * decode_fp8 (_patches/_common.py:249-273). */
+int c4q_fp8_dequant(const uint8_t* w, int64_t n, const float* scale, void* out,
+                    int out_dtype, void* stream);
+
+/* W8A16 linear: D[M,N] = out_dtype(A@W'^T + f32(bias[n])) with
+ * A [M,K] bf16 or f16 and W [N,K] e4m3fn dequantized in registers to the
+ * activation type, W' = T(decode(W) * T(w_scale[0])) (w_scale NULL = plain
+ * decode). act_table (bf16 output only, or NULL): 65,536 bf16 entries applied
+ * to the rounded output (e.g. GELU-tanh for an MLP up-projection).
+ * Replaces w8a16_bias_bf16 / w8a16_f32
+ * (_patches/fp8s_ext/w8a16_gemm.mm:286-314) behind _w8a16_forward
+ * (_patches/linear_fp8_w8a16.py:151-196). */
+int c4q_w8a16_gemm_nt(const void* a, int a_dtype, int64_t lda, const uint8_t* w, int64_t ldw,
+                      const float* w_scale, void* d, int d_dtype, int64_t ldd,
+                      const void* bias, int bias_dtype, const uint16_t* act_table,
+                      int64_t M, int64_t N, int64_t K, void* stream);
+
+/* Fused gate/up FFN pair, bf16 out [M, N_out]:
+ *   x1 = bf16(f32(A@Wg^T) * (gate_scale[c] * row_scale[m]))
+ *   x2 = bf16(f32(A@Wu^T) * (up_scale[c] * row_scale[m]))
+ *   D  = bf16(f32(T1[x1]) * f32(T2[x2]))   (NULL table = identity)
+ * Wg, Wu: int8 [N_out, K] with row stride ldw. Krea2 SwiGLU: T1 = SiLU
+ * table, T2 = NULL. MOSS FC1/SiTU: Wg/Wu = the hidden/gate halves of one
+ * [2F, K] weight, T1/T2 = its SiTU tables.
+ * Replaces pair_128_128_4_4_0 (_patches/krea2_ffn_pair.metal:281-304) and
+ * fc1_situ (_patches/moss_ffn_mps.metal:278-301). */
+int c4q_i8_ffn_pair(const int8_t* a, int64_t lda, const int8_t* w_gate, const int8_t* w_up,
+                    int64_t ldw, uint16_t* d, int64_t ldd, const float* row_scale,
+                    const float* gate_scale, const float* up_scale,
+                    const uint16_t* table_gate, const uint16_t* table_up,
+                    int64_t M, int64_t N_out, int64_t K, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CDNA4Q_H */
