@@ -1,0 +1,373 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantized linear path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only C2,C4,...]
+
+Prints ONE JSON line. The headline (``value``) is BASELINE config C2: the
+FLUX-style DiT W8A16 step, i.e. the fused-QKV (3072->9216) and out-proj
+(3072->3072) fp8-e4m3fn-weight linears over X [2*4608, 3072] bf16, in
+TFLOP/s (2*M*K*N per linear). ``roofline`` covers the dominant kernel of
+that step (the QKV W8A16 GEMM), timed with HIP events around each of its
+launches inside the timed region. ``per_config`` adds C1, C3, C4 and C5
+measured in the same process; ``cpu_baseline`` times the reference's
+PyTorch CPU path for C2 (kitchen dequant + bf16 F.linear) on a bounded row
+sample on this host's cores.
+
+Inputs are synthetic, generated from fixed seeds directly in HBM before the
+timed region; weights are random-init N(0, 0.02) quantized the way each
+config specifies.
+"""
+import argparse
+import importlib.util
+import json
+import os
+import pathlib
+import statistics
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+PKG_DIR = ROOT / "comfyui-applesilicon-optimized_amd"
+
+METRIC = "quantized GEMM TOPS + % of MFMA peak on FLUX-shape DiT linears (INT8/FP8)"
+# MI355X published dense peaks
+PEAK = {"bf16": 2500.0, "fp8": 5000.0, "int8": 5000.0, "hbm_gbs": 8000.0}
+
+
+def load_package():
+    if "cdna4q" in sys.modules:
+        return sys.modules["cdna4q"]
+    spec = importlib.util.spec_from_file_location(
+        "cdna4q", PKG_DIR / "__init__.py", submodule_search_locations=[str(PKG_DIR)])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["cdna4q"] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+class Timer:
+    """Wall time of K steps between device synchronizations, plus HIP-event
+    time of one marked launch per step (events are recorded on the current
+    stream, which is the stream every cdna4q call enqueues on)."""
+
+    def __init__(self, torch):
+        self.torch = torch
+
+    def run(self, step, steps, warmup):
+        torch = self.torch
+        for _ in range(warmup):
+            step(None)
+        pairs = [[torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True), False]
+                 for _ in range(steps)]
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(steps):
+            step(pairs[i])
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) / steps
+        kern = [a.elapsed_time(b) / 1e3 for a, b, rec in pairs if rec]
+        kern_t = statistics.mean(kern) if kern else None
+        return wall, kern_t
+
+
+def marked(pair, fn):
+    if pair is None:
+        return fn()
+    pair[0].record()
+    r = fn()
+    pair[1].record()
+    pair[2] = True
+    return r
+
+
+def fp8_pertensor(torch, w):
+    s = w.abs().amax().float() / 448.0
+    q = (w / s).clamp(-448, 448).to(torch.float8_e4m3fn)
+    return q, s.reshape(1)
+
+
+# ----------------------------------------------------------------- C2 ---
+
+def make_c2(torch, dev, M=9216, K=3072, Ns=(9216, 3072), seed=2):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+    layers = []
+    for n in Ns:
+        w = 0.02 * torch.randn(n, K, generator=g, device=dev)
+        q, s = fp8_pertensor(torch, w)
+        b = (0.01 * torch.randn(n, generator=g, device=dev)).to(torch.bfloat16)
+        layers.append((q, s, b))
+        del w
+    return x, layers
+
+
+def bench_c2(torch, ops, dev, steps, warmup):
+    M, K, Ns = 9216, 3072, (9216, 3072)
+    x, layers = make_c2(torch, dev, M, K, Ns)
+
+    def step(pair):
+        q, s, b = layers[0]
+        marked(pair, lambda: ops.w8a16_linear(x, q, s, b))
+        q, s, b = layers[1]
+        ops.w8a16_linear(x, q, s, b)
+
+    wall, kern = Timer(torch).run(step, steps, warmup)
+    flops = sum(2.0 * M * K * n for n in Ns)
+    qkv_flops = 2.0 * M * K * Ns[0]
+    return {
+        "flops": flops, "wall_s": wall, "tflops": flops / wall / 1e12,
+        "kernel": "W8A16 GEMM (256x256 tile) fused-QKV 9216x3072 -> 9216",
+        "kernel_s": kern, "kernel_flops": qkv_flops,
+        "kernel_tflops": qkv_flops / kern / 1e12 if kern else None,
+    }
+
+
+def cpu_baseline_c2(torch, budget_s=12.0):
+    """The reference's CPU path (kitchen dequant + bf16 F.linear) on a row
+    sample of C2 sized for ~budget_s of CPU work; weights at full size."""
+    sys.path.insert(0, str(ROOT))
+    from oracle import torch_path
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count() or 1
+    env_cap = os.environ.get("OMP_NUM_THREADS")
+    if env_cap and env_cap.isdigit():
+        cores = min(cores, int(env_cap))
+    torch.set_num_threads(cores)
+    K, Ns = 3072, (9216, 3072)
+    g = torch.Generator().manual_seed(2)
+    ws = []
+    for n in Ns:
+        w = 0.02 * torch.randn(n, K, generator=g)
+        q, s = fp8_pertensor(torch, w)
+        ws.append((q, s, (0.01 * torch.randn(n, generator=g)).to(torch.bfloat16)))
+
+    def run(rows):
+        x = torch.randn(rows, K, generator=g).to(torch.bfloat16)
+        t0 = time.perf_counter()
+        for q, s, b in ws:
+            torch_path.c2_w8a16_linear(x, q, s, b)
+        return time.perf_counter() - t0
+
+    rows = 256
+    run(rows)                     # warm-up (thread pool, oneDNN kernels)
+    t = run(rows)
+    per_rep = budget_s / 3.0
+    rows = int(min(9216, max(256, rows * per_rep / max(t, 1e-3))))
+    rows -= rows % 64
+    t1 = run(rows)
+    reps = int(min(50, max(3, budget_s / max(t1, 1e-3))))
+    times = [t1] + [run(rows) for _ in range(reps - 1)]
+    tmed = statistics.median(times)
+    flops = sum(2.0 * rows * K * n for n in Ns)
+    try:
+        model = next((l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo")
+                      if l.startswith("model name")), "unknown")
+    except OSError:
+        model = "unknown"
+    return {
+        "value": flops / tmed / 1e12, "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"C2 step on {rows} of 9216 rows (K=3072, N=9216+3072, full-size fp8 "
+                   f"weights dequantized per call), median of {reps} reps = {tmed:.3f} s; "
+                   f"torch CPU, {model}"),
+    }
+
+
+# ----------------------------------------------------------------- C1 ---
+
+def bench_c1(torch, ops, dev, steps, warmup):
+    M, K, N = 1024, 3072, 3072
+    g = torch.Generator(device=dev).manual_seed(1)
+    x = torch.randint(-127, 128, (M, K), generator=g, device=dev, dtype=torch.int8)
+    w = torch.randint(-127, 128, (N, K), generator=g, device=dev, dtype=torch.int8)
+    rs = 0.005 + 0.015 * torch.rand(M, generator=g, device=dev)
+    cs = 0.0005 + 0.0015 * torch.rand(N, generator=g, device=dev)
+    wall, kern = Timer(torch).run(
+        lambda p: marked(p, lambda: ops.i8_matmul2d_nt_fused_cs(x, w, rs, cs)), steps, warmup)
+    ops_ = 2.0 * M * N * K
+    t = kern or wall
+    return {"shape": [M, K, N], "wall_ms": wall * 1e3, "kernel_ms": t * 1e3,
+            "tops": ops_ / t / 1e12, "frac_int8_peak": ops_ / t / 1e12 / PEAK["int8"]}
+
+
+# ----------------------------------------------------------------- C3 ---
+
+def bench_c3(torch, ops, dev, steps, warmup):
+    M = 16384
+    g = torch.Generator(device=dev).manual_seed(3)
+    out = {}
+    for name, K, N in (("up", 5120, 13824), ("down", 13824, 5120)):
+        x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+        w = 0.02 * torch.randn(N, K, generator=g, device=dev)
+        wq, ws = fp8_pertensor(torch, w)
+        del w
+        xq, xs = ops.fp8_quant_pertensor(x)
+        wt = wq.t()
+        wall, kern = Timer(torch).run(
+            lambda p: marked(p, lambda: ops.scaled_mm(xq, wt, out_dtype=torch.bfloat16,
+                                                      scale_a=xs, scale_b=ws)), steps, warmup)
+        qwall, qkern = Timer(torch).run(lambda p: marked(p, lambda: ops.fp8_quant_pertensor(x)),
+                                        max(3, steps // 2), 2)
+        fl = 2.0 * M * N * K
+        out[name] = {"shape": [M, K, N], "gemm_ms": kern * 1e3, "tflops": fl / kern / 1e12,
+                     "frac_fp8_peak": fl / kern / 1e12 / PEAK["fp8"],
+                     "act_quant_ms": qwall * 1e3,
+                     "step_tflops": fl / (kern + qwall) / 1e12}
+        del x, xq
+    return out
+
+
+# ----------------------------------------------------------------- C4 ---
+
+def bench_c4(torch, ops, dev, steps, warmup):
+    M, K, N = 8192, 3072, 12288
+    g = torch.Generator(device=dev).manual_seed(4)
+    x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+    ws = []
+    for _ in range(2):
+        w = 0.02 * torch.randn(N, K, generator=g, device=dev)
+        s = w.abs().amax(dim=1) / 127.0
+        q = torch.round(w / s[:, None]).clamp(-127, 127).to(torch.int8)
+        ws.append((q, s.float().contiguous()))
+    silu = ops.act_table("silu", dev)
+    q, rs = ops.i8_quant_rowwise(x)
+    rs = rs.reshape(-1)
+    (wg, gs), (wu, us) = ws
+    wall, kern = Timer(torch).run(
+        lambda p: marked(p, lambda: ops.ffn_pair(q, wg, wu, rs, gs, us, silu, None)), steps, warmup)
+    qwall, _ = Timer(torch).run(lambda p: ops.i8_quant_rowwise(x), max(3, steps // 2), 2)
+    ops_ = 2.0 * M * (2 * N) * K
+    return {"shape": [M, K, 2 * N], "pair_ms": kern * 1e3, "tops": ops_ / kern / 1e12,
+            "frac_int8_peak": ops_ / kern / 1e12 / PEAK["int8"], "act_quant_ms": qwall * 1e3}
+
+
+# ----------------------------------------------------------------- C5 ---
+
+def bench_c5(torch, ops, dev, steps, warmup):
+    M, H = 9216, 3072
+    g = torch.Generator(device=dev).manual_seed(5)
+    x = torch.randn(M, H, generator=g, device=dev).to(torch.bfloat16)
+    h = torch.randn(M, 4 * H, generator=g, device=dev).to(torch.bfloat16)
+    gelu = ops.act_table("gelu_tanh", dev)
+    lay = {}
+    for name, n, k in (("qkv", 3 * H, H), ("out", H, H), ("up", 4 * H, H), ("down", H, 4 * H)):
+        w = 0.02 * torch.randn(n, k, generator=g, device=dev)
+        q, s = fp8_pertensor(torch, w)
+        b = (0.01 * torch.randn(n, generator=g, device=dev)).to(torch.bfloat16)
+        lay[name] = (q, s, b)
+        del w
+
+    def step(pair):
+        ops.w8a16_linear(x, *lay["qkv"])
+        ops.w8a16_linear(x, *lay["out"])
+        marked(pair, lambda: ops.w8a16_linear(x, *lay["up"], act_table=gelu))
+        ops.w8a16_linear(h, *lay["down"])
+
+    wall, kern = Timer(torch).run(step, steps, warmup)
+    fl = 2.0 * M * H * (3 * H + H + 4 * H) + 2.0 * M * 4 * H * H
+    res = {"stack_ms": wall * 1e3, "stack_tflops": fl / wall / 1e12,
+           "frac_bf16_peak": fl / wall / 1e12 / PEAK["bf16"],
+           "mlp_up_gelu_tflops": 2.0 * M * H * 4 * H / kern / 1e12}
+    # skinny decode shapes: HBM-bound; rotate weight copies past the 256 MB MALL
+    skinny = {}
+    for n in (18432, 3072):
+        copies = max(8, int(600e6 // (n * H)) + 1)
+        wq = []
+        for _ in range(copies):
+            w = 0.02 * torch.randn(n, H, generator=g, device=dev)
+            wq.append(fp8_pertensor(torch, w))
+            del w
+        b = (0.01 * torch.randn(n, generator=g, device=dev)).to(torch.bfloat16)
+        for m in (1, 4, 16):
+            xs = torch.randn(m, H, generator=g, device=dev).to(torch.bfloat16)
+            it = {"i": 0}
+
+            def sstep(pair):
+                q, s = wq[it["i"] % copies]
+                it["i"] += 1
+                marked(pair, lambda: ops.w8a16_linear(xs, q, s, b))
+
+            wall, kern = Timer(torch).run(sstep, max(steps, copies), 2)
+            byts = n * H + m * H * 2 + m * n * 2 + n * 2
+            skinny[f"M{m}_N{n}"] = {"kernel_us": kern * 1e6, "gbs": byts / kern / 1e9,
+                                    "frac_hbm": byts / kern / 1e9 / PEAK["hbm_gbs"]}
+        del wq
+    res["skinny"] = skinny
+    return res
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--only", default="C1,C2,C3,C4,C5",
+                    help="comma list of configs to run (C2 is always run)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        log(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+            "(multi-GPU sharding is design-only).")
+        sys.exit(2)
+
+    import torch
+    load_package()
+    import cdna4q.ops as ops
+
+    dev = torch.device("cuda", 0)
+    only = {c.strip().upper() for c in args.only.split(",") if c.strip()}
+    per = {}
+    log("C2 (headline) ...")
+    c2 = bench_c2(torch, ops, dev, args.steps, args.warmup)
+    torch.cuda.empty_cache()
+    for name, fn in (("C1", bench_c1), ("C3", bench_c3), ("C4", bench_c4), ("C5", bench_c5)):
+        if name in only:
+            log(f"{name} ...")
+            per[name] = fn(torch, ops, dev, args.steps, args.warmup)
+            torch.cuda.empty_cache()
+    per["C2"] = {"step_ms": c2["wall_s"] * 1e3, "tflops": c2["tflops"],
+                 "frac_bf16_peak": c2["tflops"] / PEAK["bf16"],
+                 "qkv_kernel_ms": c2["kernel_s"] * 1e3, "qkv_kernel_tflops": c2["kernel_tflops"]}
+
+    cpu = None
+    if not args.no_cpu:
+        log("CPU baseline (reference torch CPU path, C2 sample) ...")
+        cpu = cpu_baseline_c2(torch)
+
+    kt = c2["kernel_tflops"]
+    line = {
+        "metric": METRIC,
+        "value": round(c2["tflops"], 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(c2["wall_s"] * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": ("synthetic: seeded N(0,1) bf16 activations, N(0,0.02) weights quantized to "
+                 "e4m3fn with per-tensor amax/448 scales, N(0,0.01) bf16 bias"),
+        "config": {"workload": ("C2: FLUX DiT W8A16 fused-QKV (3072->9216) + out-proj "
+                                "(3072->3072) linears over X[2*4608, 3072] bf16, fp8 e4m3fn "
+                                "per-tensor weights dequantized in registers, bf16 out"),
+                   "M": 9216, "K": 3072, "N": [9216, 3072]},
+        "roofline": {"bound": "mfma", "achieved": round(kt, 2) if kt else None,
+                     "peak": PEAK["bf16"], "unit": "TFLOP/s",
+                     "frac": round(kt / PEAK["bf16"], 4) if kt else None, "traffic": None,
+                     "kernel": c2["kernel"]},
+        "cpu_baseline": cpu,
+        "per_config": per,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()
