@@ -27,16 +27,9 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-// Output-tile shapes of the tiled kernels. Larger tiles reuse each staged
-// operand byte across more MFMAs; smaller ones make more workgroups for
-// shapes that would otherwise leave CUs idle.
-enum TileCfg { TILE_256x256 = 0, TILE_128x128 = 1, TILE_64x128 = 2 };
-
-inline TileCfg pick_tile(int64_t M, int64_t N) {
-  const int64_t cus = 256;
-  if (cdiv(M, 256) * cdiv(N, 256) >= 2 * cus) return TILE_256x256;
-  if (cdiv(M, 128) * cdiv(N, 128) >= cus) return TILE_128x128;
-  return TILE_64x128;
+// Output rows can take 16-byte stores: aligned base, row pitch a multiple of 16.
+inline int rows_vec16(const void* d, int64_t ld, int64_t elem_bytes) {
+  return aligned16(d) && (ld * elem_bytes) % 16 == 0 ? 1 : 0;
 }
 
 }  // namespace c4q

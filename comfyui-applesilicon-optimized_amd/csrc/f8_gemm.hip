@@ -13,25 +13,13 @@ template <bool BF16, bool HAS_SCALE, class Epi>
 int run_w8a16_tiled(const uint16_t* a, int64_t lda, const uint8_t* w, int64_t ldw,
                     const float* w_scale, int64_t M, int64_t N, int64_t K, const Epi& epi,
                     hipStream_t s, const char* what) {
-  using Mma = typename std::conditional<BF16, MmaBF16, MmaF16>::type;
-  GemmShape sh{M, N, K, 2 * K, K, 0, 0};
-  RowsPlain ra{reinterpret_cast<const uint8_t*>(a), 2 * lda, M};
-  RowsPlain rb{w, ldw, N};
-  BStoreDequant<BF16> bst{w_scale, 1.0f};
-  switch (pick_tile(M, N)) {
-    case TILE_256x256:
-      return launch_tile<Mma, 256, 256, Load8<256, RowsPlain>, RowsPlain,
-                         LoadW8<256, BF16, HAS_SCALE>, RowsPlain, BStoreDequant<BF16>, false>(
-          sh, N, ra, rb, bst, epi, s, what);
-    case TILE_128x128:
-      return launch_tile<Mma, 128, 128, Load8<128, RowsPlain>, RowsPlain,
-                         LoadW8<128, BF16, HAS_SCALE>, RowsPlain, BStoreDequant<BF16>, false>(
-          sh, N, ra, rb, bst, epi, s, what);
-    default:
-      return launch_tile<Mma, 64, 128, Load8<64, RowsPlain>, RowsPlain,
-                         LoadW8<128, BF16, HAS_SCALE>, RowsPlain, BStoreDequant<BF16>, false>(
-          sh, N, ra, rb, bst, epi, s, what);
-  }
+  GemmShape sh{M, N, K, 0, 0};
+  const Src2 sa{reinterpret_cast<const uint8_t*>(a), reinterpret_cast<const uint8_t*>(a), 2 * lda, M};
+  const Src2 sb{w, w, ldw, N};
+  return with_tile(pick_tile(M, N), [&](auto t) {
+    using T = decltype(t);
+    return launch_tile<T, OpW8A16<BF16, HAS_SCALE>, false>(sh, N, sa, sb, w_scale, epi, s, what);
+  });
 }
 
 }  // namespace
@@ -53,10 +41,37 @@ extern "C" int c4q_f8_gemm_nt_scaled(const uint8_t* a, int64_t lda, const uint8_
   C4Q_REQUIRE(!bias || valid_dt(bias_dtype), C4Q_ERR_ARG, "%s: bad bias dtype", what);
   if (M == 0 || N == 0) return C4Q_OK;
   C4Q_REQUIRE(d && (K == 0 || (a && b)), C4Q_ERR_ARG, "%s: null pointer", what);
-  EpiScaled epi{d, ldd, d_dtype, scale_a, scale_a_mode, scale_b, scale_b_mode, scale_result,
-                bias, bias_dtype, 1.0f, 1.0f, 1.0f};
-  return run_gemm8<MmaF8, GenF8>(a, lda, b, ldb, M, N, K, epi, as_stream(stream), what);
+  if (d_dtype == C4Q_F32) {
+    EpiScaled<true> epi{{d, ldd, rows_vec16(d, ldd, 4)}, d_dtype, scale_a, scale_a_mode, scale_b,
+                        scale_b_mode, scale_result, bias, bias_dtype, 1.0f, 1.0f, 1.0f};
+    return run_gemm8<OpF8, GenF8>(a, lda, b, ldb, M, N, K, epi, as_stream(stream), what);
+  }
+  EpiScaled<false> epi{{d, ldd, rows_vec16(d, ldd, 2)}, d_dtype, scale_a, scale_a_mode, scale_b,
+                       scale_b_mode, scale_result, bias, bias_dtype, 1.0f, 1.0f, 1.0f};
+  return run_gemm8<OpF8, GenF8>(a, lda, b, ldb, M, N, K, epi, as_stream(stream), what);
 }
+
+namespace {
+template <class Epi>
+int run_w8a16(const void* a, int a_dtype, int64_t lda, const uint8_t* w, int64_t ldw,
+              const float* w_scale, int64_t M, int64_t N, int64_t K, const Epi& epi, hipStream_t s,
+              const char* what) {
+  const bool bf16 = a_dtype == C4Q_BF16;
+  const bool tiled = K > 0 && K % 16 == 0 && aligned16(a) && aligned16(w) && lda % 8 == 0 &&
+                     ldw % 16 == 0 && tile_offsets_fit(2 * lda, ldw);
+  if (!tiled) {
+    GenW8A16 op{static_cast<const uint16_t*>(a), lda, w, ldw, w_scale, bf16 ? 1 : 0, 1.0f};
+    return launch_generic(M, N, K, op, epi, s, what);
+  }
+  const uint16_t* a16 = static_cast<const uint16_t*>(a);
+  if (bf16) {
+    return w_scale ? run_w8a16_tiled<true, true>(a16, lda, w, ldw, w_scale, M, N, K, epi, s, what)
+                   : run_w8a16_tiled<true, false>(a16, lda, w, ldw, w_scale, M, N, K, epi, s, what);
+  }
+  return w_scale ? run_w8a16_tiled<false, true>(a16, lda, w, ldw, w_scale, M, N, K, epi, s, what)
+                 : run_w8a16_tiled<false, false>(a16, lda, w, ldw, w_scale, M, N, K, epi, s, what);
+}
+}  // namespace
 
 extern "C" int c4q_w8a16_gemm_nt(const void* a, int a_dtype, int64_t lda, const uint8_t* w,
                                  int64_t ldw, const float* w_scale, void* d, int d_dtype,
@@ -76,19 +91,10 @@ extern "C" int c4q_w8a16_gemm_nt(const void* a, int a_dtype, int64_t lda, const 
   if (M == 0 || N == 0) return C4Q_OK;
   C4Q_REQUIRE(d && (K == 0 || (a && w)), C4Q_ERR_ARG, "%s: null pointer", what);
   hipStream_t s = as_stream(stream);
-  EpiW8A16 epi{d, ldd, d_dtype, bias, bias_dtype, act_table};
-  const bool bf16 = a_dtype == C4Q_BF16;
-  const bool tiled = K > 0 && K % 16 == 0 && aligned16(a) && aligned16(w) && lda % 8 == 0 &&
-                     ldw % 16 == 0;
-  if (!tiled) {
-    GenW8A16 op{static_cast<const uint16_t*>(a), lda, w, ldw, w_scale, bf16 ? 1 : 0, 1.0f};
-    return launch_generic(M, N, K, op, epi, s, what);
+  if (d_dtype == C4Q_F32) {
+    EpiW8A16<true> epi{{d, ldd, rows_vec16(d, ldd, 4)}, d_dtype, bias, bias_dtype, act_table};
+    return run_w8a16(a, a_dtype, lda, w, ldw, w_scale, M, N, K, epi, s, what);
   }
-  const uint16_t* a16 = static_cast<const uint16_t*>(a);
-  if (bf16) {
-    return w_scale ? run_w8a16_tiled<true, true>(a16, lda, w, ldw, w_scale, M, N, K, epi, s, what)
-                   : run_w8a16_tiled<true, false>(a16, lda, w, ldw, w_scale, M, N, K, epi, s, what);
-  }
-  return w_scale ? run_w8a16_tiled<false, true>(a16, lda, w, ldw, w_scale, M, N, K, epi, s, what)
-                 : run_w8a16_tiled<false, false>(a16, lda, w, ldw, w_scale, M, N, K, epi, s, what);
+  EpiW8A16<false> epi{{d, ldd, rows_vec16(d, ldd, 2)}, d_dtype, bias, bias_dtype, act_table};
+  return run_w8a16(a, a_dtype, lda, w, ldw, w_scale, M, N, K, epi, s, what);
 }

@@ -6,25 +6,34 @@
 // layout [N, K]; both are K-contiguous, which is the operand order every
 // MFMA wants, so neither is ever transposed.
 //
-// Structure (one workgroup = 4 wave64s in a 2x2 arrangement):
-//   * the workgroup owns a BM x BN output tile; each wave a (BM/2) x (BN/2)
-//     sub-tile built from 32x32 MFMA blocks held in accumulator registers;
-//   * K advances in stages of 128 bytes per tile row (128 int8/fp8 values,
-//     or 64 bf16/f16 values). Each stage is staged through LDS with 16-byte
-//     global loads (a wave reads whole 128-byte rows) and double buffered:
-//     the loads of stage k+1 are in flight while stage k feeds the MFMAs,
-//     one barrier per stage;
-//   * LDS rows are 128 bytes with the 16-byte chunks XOR-swizzled by row so
-//     that the MFMA fragment reads (32 rows, one chunk) hit distinct banks;
+// Structure:
+//   * a workgroup of WM x WN wave64s owns a BM x BN output tile; each wave a
+//     (BM/WM) x (BN/WN) sub-tile of 32x32 MFMA blocks held in registers;
+//   * K advances in stages of 64 elements. Operands are copied global ->
+//     LDS by buffer_load_dwordx4 ... lds (no register round trip) into a
+//     ring of NBUF stage buffers, issued up to NBUF-1 stages ahead of the
+//     MFMAs that consume them, so the copy latency (~1.3 us from L2/MALL)
+//     hides behind several stages of MFMA work; one barrier per stage;
+//   * inside a stage the LDS fragments of the next K step are read while the
+//     current step multiplies, across stage boundaries too;
+//   * the epilogue stages each wave's output strip through LDS so that
+//     global stores are whole 16-byte chunks of output rows;
+//   * the copy reads through buffer resources based at the tile origin whose
+//     range ends at the matrix end: tail rows and the K tail read as zero in
+//     hardware (stages past K are issued with out-of-range offsets, so every
+//     stage issues the same number of copies);
+//   * LDS rows are 64 or 128 bytes per stage with the 16-byte chunks
+//     XOR-swizzled by row, so that fragment reads (32 lanes on 32 rows, one
+//     chunk) are bank-conflict free;
+//   * W8A16: the fp8 weight is staged as fp8 and dequantized to bf16/f16 in
+//     registers right after each fragment read (one ds_read_b128 of 16 codes
+//     feeds two K steps);
 //   * workgroup ids are remapped so that each of the 8 XCDs owns a
-//     contiguous run of tiles, walked in GROUP_M-row bands, keeping the A
-//     and B panels a band shares inside that XCD's L2.
-//
-// Operand policies supply the MFMA (int8 32x32x32, fp8 32x32x64 f8f6f4,
-// bf16/f16 32x32x16); stage loaders supply the global->LDS copy (including
-// the fp8->bf16 dequant of W8A16 weights and the gate/up row pairing of the
-// FFN-pair kernel); epilogue functors consume the accumulators.
+//     contiguous run of tiles, walked in kGroupM-row bands, keeping the A and
+//     B panels a band shares inside that XCD's L2.
 #pragma once
+#include <type_traits>
+
 #include "numerics.hpp"
 
 namespace c4q {
@@ -39,104 +48,80 @@ typedef __bf16   bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8  __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2  __attribute__((ext_vector_type(2)));
 
-constexpr int kThreads = 256;
-constexpr int kRowBytes = 128;       // LDS bytes per tile row per stage
+constexpr int kStageK = 64;          // K elements per pipeline stage
 constexpr int kGroupM = 8;           // tile rows per raster band
 
 template <class T, class F>
 __device__ __forceinline__ T bitcast(const F& f) { return __builtin_bit_cast(T, f); }
 
-// physical 16-byte chunk of logical chunk c in LDS row r
-__device__ __forceinline__ int swz_chunk(int r, int c) { return c ^ (r & 7); }
+// ------------------------------------------------------------ swizzles ---
+// Physical 16-byte chunk of logical chunk c in LDS row r. A fragment read
+// has 32 consecutive lanes on 32 consecutive rows at one logical chunk; the
+// row permutations below send any 8 consecutive rows to 8 distinct 16-byte
+// bank groups of a 128-byte window and any 16 consecutive rows to 16
+// distinct groups of a 256-byte window, so ds_read_b128 is conflict-free
+// whether the LDS serves 8 or 16 lanes per cycle.
+template <int ROWB> struct Swz;
+template <> struct Swz<128> {   // 8 chunks per row
+  __device__ __forceinline__ static int f(int r) { return ((r >> 1) ^ ((r & 1) << 2)) & 7; }
+};
+template <> struct Swz<64> {    // 4 chunks per row
+  __device__ __forceinline__ static int f(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
+};
+template <int ROWB>
+__device__ __forceinline__ int phys_chunk(int r, int c) { return c ^ Swz<ROWB>::f(r); }
 
-// ---------------------------------------------------------------- MFMA ---
-struct MmaI8 {
-  using Acc = i32x16;
-  using Scalar = int32_t;
-  static constexpr int kChunks = 1;           // 16-byte chunks per lane fragment
-  __device__ static Acc mma(const i32x4* a, const i32x4* b, Acc c) {
-    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a[0], b[0], c, 0, 0, 0);
-  }
-};
-struct MmaF8 {                                 // OCP e4m3 x e4m3, fp32 accumulate
-  using Acc = f32x16;
-  using Scalar = float;
-  static constexpr int kChunks = 2;
-  __device__ static Acc mma(const i32x4* a, const i32x4* b, Acc c) {
-    i32x8 av = {a[0].x, a[0].y, a[0].z, a[0].w, a[1].x, a[1].y, a[1].z, a[1].w};
-    i32x8 bv = {b[0].x, b[0].y, b[0].z, b[0].w, b[1].x, b[1].y, b[1].z, b[1].w};
-    // cbsz = blgp = 0 select e4m3 for both operands; zero scales select the
-    // unscaled multiply.
-    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, bv, c, 0, 0, 0, 0, 0, 0);
-  }
-};
-struct MmaBF16 {
-  using Acc = f32x16;
-  using Scalar = float;
-  static constexpr int kChunks = 1;
-  __device__ static Acc mma(const i32x4* a, const i32x4* b, Acc c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(bitcast<bf16x8>(a[0]), bitcast<bf16x8>(b[0]), c, 0, 0, 0);
-  }
-};
-struct MmaF16 {
-  using Acc = f32x16;
-  using Scalar = float;
-  static constexpr int kChunks = 1;
-  __device__ static Acc mma(const i32x4* a, const i32x4* b, Acc c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(bitcast<f16x8>(a[0]), bitcast<f16x8>(b[0]), c, 0, 0, 0);
-  }
-};
+// ------------------------------------------------------------- buffers ---
+// Buffer resource (V#) over [base, base + bytes); offsets at or past the
+// range read zeros. Ranges are clamped below 2^31 (a tile spans <= 256 rows,
+// so its offsets stay far below that).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const uint8_t* base, int64_t bytes) {
+  const int32_t n = bytes > 0x7FFFFFF0ll ? 0x7FFFFFF0 : (int32_t)(bytes < 0 ? 0 : bytes);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(base), (short)0, n, 0x00020000);
+}
+constexpr int kOOB = 0x7FFFFFF0;   // an offset past any range
 
-// ------------------------------------------------------- stage loaders ---
-// Row sources map a tile row to a global row pointer (already clamped into
-// range: rows past the end re-read the last row; their results are never
-// stored).
-struct RowsPlain {
-  const uint8_t* base; int64_t ld_bytes; int64_t rows;
-  __device__ __forceinline__ const uint8_t* row(int64_t r) const {
-    return base + (r < rows ? r : rows - 1) * ld_bytes;
-  }
-};
-// FFN pair: in the doubled-N space every 32-row MFMA block alternates
-// between gate rows (even blocks) and up rows (odd blocks) of the same 32
-// output columns, so one lane ends up holding gate and up accumulators of
-// the same (m, col).
-struct RowsPair {
-  const uint8_t* gate; const uint8_t* up; int64_t ld_bytes; int64_t rows;  // rows = N_out
-  __device__ __forceinline__ const uint8_t* row(int64_t r2) const {
-    int64_t blk = r2 >> 5;
-    int64_t col = ((blk >> 1) << 5) + (r2 & 31);
-    col = col < rows ? col : rows - 1;
-    return ((blk & 1) ? up : gate) + col * ld_bytes;
-  }
-};
-
-// Copies ROWS x 128 bytes per stage; every thread owns ROWS/32 chunks of
-// 16 bytes (row = tid/8 + 32 i, chunk = tid % 8). K is masked at 16-byte
-// granularity (chunks at or past k_bytes load zeros).
-template <int ROWS, class Src>
-struct Load8 {
-  static constexpr int kN = ROWS * 8 / kThreads;
-  i32x4 v[kN];
-  __device__ __forceinline__ void load(const Src& src, int64_t r0, int64_t kb0, int64_t k_bytes) {
-    const int tid = threadIdx.x;
-    const int c = tid & 7;
-    const int64_t kb = kb0 + c * 16;
-    const bool ok = kb < k_bytes;
+// Direct global->LDS copy of one stage of a ROWS x ROWB-byte operand slab.
+// One buffer_load_dwordx4 ... lds moves 1 KB: lane L fills LDS row
+// RPI*q + L/CPR at physical chunk L%CPR, so it fetches the logical chunk
+// that the swizzle stores there -- the layout comes from choosing sources.
+// PAIR (FFN gate/up): in the doubled-N tile space every 32-row MFMA block
+// alternates between the gate matrix (even blocks) and the up matrix (odd
+// blocks) for the same 32 output columns, so one lane ends up holding gate
+// and up accumulators of the same (m, col).
+template <int ROWS, int ROWB, int NT, bool PAIR>
+struct DirectLoad {
+  static constexpr int CPR = ROWB / 16;             // chunks per row
+  static constexpr int RPI = 64 / CPR;              // rows per instruction
+  static constexpr int kWaves = NT / 64;
+  static constexpr int kInstr = ROWS / RPI / kWaves;
+  static_assert(kInstr >= 1 && kInstr * RPI * kWaves == ROWS, "tile rows must split over the waves");
+  int voff[kInstr];
+  int kofs[kInstr];           // byte offset of this lane's chunk within the stage row
+  __device__ __forceinline__ void init(int64_t ld_bytes) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
-    for (int i = 0; i < kN; ++i) {
-      const int r = (tid >> 3) + 32 * i;
-      if (ok) v[i] = *reinterpret_cast<const i32x4*>(src.row(r0 + r) + kb);
-      else v[i] = i32x4{0, 0, 0, 0};
+    for (int j = 0; j < kInstr; ++j) {
+      const int q = wave + kWaves * j;
+      const int r = RPI * q + lane / CPR;                      // LDS row
+      const int blk = (RPI * q) >> 5;
+      const int src = PAIR ? ((blk >> 1) * 32 + ((RPI * q) & 31) + lane / CPR) : r;
+      kofs[j] = ((lane % CPR) ^ Swz<ROWB>::f(r)) * 16;
+      voff[j] = (int)(src * ld_bytes) + kofs[j];
     }
   }
-  __device__ __forceinline__ void store(uint8_t* lds) const {
-    const int tid = threadIdx.x;
-    const int c = tid & 7;
+  // Copy K bytes [kb, kb + ROWB) of every row into `lds`; bytes at or past
+  // k_bytes read zeros.
+  __device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t r0, __amdgpu_buffer_rsrc_t r1,
+                                        uint8_t* lds, int kb, int k_bytes) const {
+    const int wave = threadIdx.x >> 6;
 #pragma unroll
-    for (int i = 0; i < kN; ++i) {
-      const int r = (tid >> 3) + 32 * i;
-      *reinterpret_cast<i32x4*>(lds + r * kRowBytes + swz_chunk(r, c) * 16) = v[i];
+    for (int j = 0; j < kInstr; ++j) {
+      const int q = wave + kWaves * j;
+      const __amdgpu_buffer_rsrc_t rs = (PAIR && (((RPI * q) >> 5) & 1)) ? r1 : r0;
+      const int vo = kb + kofs[j] < k_bytes ? voff[j] : kOOB;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rs, (__attribute__((address_space(3))) void*)(lds + (RPI * q) * ROWB), 16, vo, kb, 0, 0);
     }
   }
 };
@@ -162,41 +147,133 @@ __device__ __forceinline__ void dequant4(uint32_t w, float s, uint32_t& lo, uint
   }
 }
 
-// W8A16 weight stage: 64 fp8 values (64 bytes) per row per stage expand to
-// 64 halves (128 LDS bytes). Every thread owns ROWS/64 source chunks of 16
-// codes (row = tid/4 + 64 i, source chunk = tid % 4 -> LDS chunks 2c, 2c+1).
-template <int ROWS, bool BF16, bool HAS_SCALE>
-struct LoadW8 {
-  static constexpr int kN = ROWS * 4 / kThreads;
-  i32x4 v[kN];
-  __device__ __forceinline__ void load(const RowsPlain& src, int64_t r0, int64_t kb0, int64_t k_bytes) {
-    const int tid = threadIdx.x;
-    const int c = tid & 3;
-    const int64_t kb = kb0 + c * 16;
-    const bool ok = kb < k_bytes;
+// ------------------------------------------------------ operand policies ---
+// Each policy fixes the MFMA, the stage row sizes of A and B in LDS (SA, SB
+// bytes per row per stage) and how one stage's fragments are read and
+// multiplied.
+template <int ROWB>
+__device__ __forceinline__ i32x4 lds_chunk(const uint8_t* sm, int r, int c) {
+  return *reinterpret_cast<const i32x4*>(sm + r * ROWB + phys_chunk<ROWB>(r, c) * 16);
+}
+
+// Policies expose one stage as S "K steps": frags(s) reads the LDS
+// fragments of step s into registers, mma(frags) multiplies them. The
+// kernel reads step s+1 while step s multiplies.
+
+// int8 x int8 -> int32, v_mfma_i32_32x32x32_i8: a lane holds 16 K values
+// (one chunk); a 64-byte stage row is 2 K steps.
+struct OpI8 {
+  using Acc = i32x16;
+  static constexpr int SA = 64, SB = 64, S = 2;
+  template <int TM, int TN> struct Frag { i32x4 a[TM], b[TN]; };
+  __device__ __forceinline__ static float prep_scale(const float*) { return 1.0f; }
+  template <int TM, int TN>
+  __device__ __forceinline__ static void frags(Frag<TM, TN>& f, const uint8_t* sa, const uint8_t* sb,
+                                               int ra0, int rb0, int s) {
+    const int lane = threadIdx.x & 63, lr = lane & 31, h = lane >> 5;
 #pragma unroll
-    for (int i = 0; i < kN; ++i) {
-      const int r = (tid >> 2) + 64 * i;
-      if (ok) v[i] = *reinterpret_cast<const i32x4*>(src.row(r0 + r) + kb);
-      else v[i] = i32x4{0, 0, 0, 0};
+    for (int i = 0; i < TM; ++i) f.a[i] = lds_chunk<SA>(sa, ra0 + i * 32 + lr, 2 * s + h);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) f.b[j] = lds_chunk<SB>(sb, rb0 + j * 32 + lr, 2 * s + h);
+  }
+  template <int TM, int TN>
+  __device__ __forceinline__ static void mma(const Frag<TM, TN>& f, Acc (&acc)[TM][TN], float) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
+  }
+};
+
+// OCP e4m3 x e4m3 -> fp32, v_mfma_f32_32x32x64_f8f6f4 (cbsz = blgp = 0:
+// e4m3 operands; zero scales: unscaled): a lane holds 32 K values (two
+// chunks); a 64-byte stage row is one K step.
+struct OpF8 {
+  using Acc = f32x16;
+  static constexpr int SA = 64, SB = 64, S = 1;
+  template <int TM, int TN> struct Frag { i32x8 a[TM], b[TN]; };
+  __device__ __forceinline__ static float prep_scale(const float*) { return 1.0f; }
+  template <int TM, int TN>
+  __device__ __forceinline__ static void frags(Frag<TM, TN>& f, const uint8_t* sa, const uint8_t* sb,
+                                               int ra0, int rb0, int) {
+    const int lane = threadIdx.x & 63, lr = lane & 31, h = lane >> 5;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const i32x4 x = lds_chunk<SA>(sa, ra0 + i * 32 + lr, 2 * h);
+      const i32x4 y = lds_chunk<SA>(sa, ra0 + i * 32 + lr, 2 * h + 1);
+      f.a[i] = i32x8{x.x, x.y, x.z, x.w, y.x, y.y, y.z, y.w};
+    }
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const i32x4 x = lds_chunk<SB>(sb, rb0 + j * 32 + lr, 2 * h);
+      const i32x4 y = lds_chunk<SB>(sb, rb0 + j * 32 + lr, 2 * h + 1);
+      f.b[j] = i32x8{x.x, x.y, x.z, x.w, y.x, y.y, y.z, y.w};
     }
   }
-  __device__ __forceinline__ void store(uint8_t* lds, float s) const {
-    const int tid = threadIdx.x;
-    const int c = tid & 3;
+  template <int TM, int TN>
+  __device__ __forceinline__ static void mma(const Frag<TM, TN>& f, Acc (&acc)[TM][TN], float) {
 #pragma unroll
-    for (int i = 0; i < kN; ++i) {
-      const int r = (tid >> 2) + 64 * i;
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.a[i], f.b[j], acc[i][j], 0, 0,
+                                                                    0, 0, 0, 0);
+  }
+};
+
+// W8A16: bf16 (or f16) activations x fp8 weights dequantized in registers,
+// v_mfma_f32_32x32x16_{bf16,f16}: a lane holds 8 K values. A stage row is
+// 128 bytes of activations and 64 bytes of fp8 weights (64 K values = 4
+// MFMA steps, taken here as 2 K steps of 2 MFMAs). The K order inside a
+// stage is permuted identically for both operands: K step t, lane half h,
+// takes the 16 consecutive K values [32t + 16h, 32t + 16h + 16) -- the first
+// 8 in its first MFMA, the last 8 in its second -- so one 16-byte fp8 chunk
+// (chunk 2t+h) feeds both, while the activation fragments are bf16 chunks
+// 4t + 2h and 4t + 2h + 1.
+template <bool BF16, bool HAS_SCALE>
+struct OpW8A16 {
+  using Acc = f32x16;
+  static constexpr int SA = 128, SB = 64, S = 2;
+  template <int TM, int TN> struct Frag { i32x4 a[2][TM], q[TN]; };
+  // per-tensor weight scale rounded to the activation type (scale.to(T))
+  __device__ __forceinline__ static float prep_scale(const float* sp) {
+    if (!HAS_SCALE || !sp) return 1.0f;
+    return BF16 ? bf16_f32(bf16_rte(sp[0])) : f16_f32(f16_rte(sp[0]));
+  }
+  __device__ __forceinline__ static f32x16 mfma(i32x4 a, i32x4 b, f32x16 c) {
+    if constexpr (BF16)
+      return __builtin_amdgcn_mfma_f32_32x32x16_bf16(bitcast<bf16x8>(a), bitcast<bf16x8>(b), c, 0, 0, 0);
+    else
+      return __builtin_amdgcn_mfma_f32_32x32x16_f16(bitcast<f16x8>(a), bitcast<f16x8>(b), c, 0, 0, 0);
+  }
+  template <int TM, int TN>
+  __device__ __forceinline__ static void frags(Frag<TM, TN>& f, const uint8_t* sa, const uint8_t* sb,
+                                               int ra0, int rb0, int t) {
+    const int lane = threadIdx.x & 63, lr = lane & 31, h = lane >> 5;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) f.q[j] = lds_chunk<SB>(sb, rb0 + j * 32 + lr, 2 * t + h);
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int i = 0; i < TM; ++i) f.a[u][i] = lds_chunk<SA>(sa, ra0 + i * 32 + lr, 4 * t + 2 * h + u);
+  }
+  template <int TM, int TN>
+  __device__ __forceinline__ static void mma(const Frag<TM, TN>& f, Acc (&acc)[TM][TN], float ws) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
       uint32_t o[8];
-      dequant4<BF16, HAS_SCALE>((uint32_t)v[i].x, s, o[0], o[1]);
-      dequant4<BF16, HAS_SCALE>((uint32_t)v[i].y, s, o[2], o[3]);
-      dequant4<BF16, HAS_SCALE>((uint32_t)v[i].z, s, o[4], o[5]);
-      dequant4<BF16, HAS_SCALE>((uint32_t)v[i].w, s, o[6], o[7]);
-      uint8_t* row = lds + r * kRowBytes;
-      *reinterpret_cast<i32x4*>(row + swz_chunk(r, 2 * c) * 16) =
-          i32x4{(int)o[0], (int)o[1], (int)o[2], (int)o[3]};
-      *reinterpret_cast<i32x4*>(row + swz_chunk(r, 2 * c + 1) * 16) =
-          i32x4{(int)o[4], (int)o[5], (int)o[6], (int)o[7]};
+      dequant4<BF16, HAS_SCALE>((uint32_t)f.q[j].x, ws, o[0], o[1]);
+      dequant4<BF16, HAS_SCALE>((uint32_t)f.q[j].y, ws, o[2], o[3]);
+      dequant4<BF16, HAS_SCALE>((uint32_t)f.q[j].z, ws, o[4], o[5]);
+      dequant4<BF16, HAS_SCALE>((uint32_t)f.q[j].w, ws, o[6], o[7]);
+      const i32x4 b0 = {(int)o[0], (int)o[1], (int)o[2], (int)o[3]};
+      const i32x4 b1 = {(int)o[4], (int)o[5], (int)o[6], (int)o[7]};
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        acc[i][j] = mfma(f.a[0][i], b0, acc[i][j]);
+        acc[i][j] = mfma(f.a[1][i], b1, acc[i][j]);
+      }
     }
   }
 };
@@ -221,115 +298,159 @@ __device__ __forceinline__ TileCoord tile_of(int bid, int nblocks, int tiles_m, 
 }
 
 // ------------------------------------------------------------ epilogue ---
-// Walk the accumulators of one wave and hand every in-range element to the
-// epilogue functor.  32x32 MFMA output layout: lane l, register r hold
-// row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+// Each wave stores its sub-tile one 32-row strip at a time through a
+// private LDS area: elements go in at their (row, column) from the MFMA
+// layout (lane l, register r hold row 8*(r/4) + 4*(l/32) + r%4, column
+// l%32 of a 32x32 block), then lanes read back whole 16-byte chunks of
+// strip rows and write them to global memory, 8..32 lanes per output row.
+// Strip rows are padded by 16 bytes so the two half-waves of a write land on
+// different banks.
+template <class OutT, int COLS>
+struct Strip {
+  static constexpr int kRowB = COLS * (int)sizeof(OutT);
+  static constexpr int kStride = kRowB + 16;
+  static constexpr int kBytes = 32 * kStride;
+  static constexpr int kCPR = kRowB / 16;                 // 16-byte chunks per row
+  static constexpr int kPerLane = 32 * kCPR / 64;
+  static_assert(kPerLane >= 1 && kPerLane * 64 == 32 * kCPR, "strip must split over a wave");
+};
+
+template <class OutT, int COLS, class Epi>
+__device__ __forceinline__ void strip_flush(const uint8_t* lds, int64_t m0, int64_t n0, int64_t M,
+                                            int64_t N, const Epi& epi) {
+  using St = Strip<OutT, COLS>;
+  constexpr int EPC = 16 / (int)sizeof(OutT);             // elements per chunk
+  const int lane = threadIdx.x & 63;
+  __builtin_amdgcn_s_waitcnt(0xc07f);                     // lgkmcnt(0): strip writes landed
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int k = 0; k < St::kPerLane; ++k) {
+    const int c = lane + 64 * k;
+    const int row = c / St::kCPR, ch = c % St::kCPR;
+    const int64_t m = m0 + row, n = n0 + ch * EPC;
+    const i32x4 v = *reinterpret_cast<const i32x4*>(lds + row * St::kStride + ch * 16);
+    if (m >= M || n >= N) continue;
+    if (epi.vec && n + EPC <= N) {
+      *reinterpret_cast<i32x4*>(epi.row(m) + n * (int64_t)sizeof(OutT)) = v;
+    } else {
+      const OutT* e = reinterpret_cast<const OutT*>(&v);
+      for (int q = 0; q < EPC && n + q < N; ++q) epi.put(m, n + q, e[q]);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);                     // reads done before the next strip
+  __builtin_amdgcn_wave_barrier();
+}
+
 template <int TM, int TN, class Acc, class Epi>
 __device__ __forceinline__ void epilogue_single(const Acc (&acc)[TM][TN], int64_t m0, int64_t n0,
-                                                int64_t M, int64_t N, const Epi& epi) {
+                                                int64_t M, int64_t N, const Epi& epi, uint8_t* lds) {
+  using OutT = typename Epi::OutT;
+  constexpr int COLS = TN * 32;
+  using St = Strip<OutT, COLS>;
   const int lane = threadIdx.x & 63;
 #pragma unroll
-  for (int j = 0; j < TN; ++j) {
-    const int64_t n = n0 + j * 32 + (lane & 31);
-    if (n >= N) continue;
+  for (int i = 0; i < TM; ++i) {
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
+    for (int j = 0; j < TN; ++j) {
+      const int col = j * 32 + (lane & 31);
+      const int64_t n = n0 + col;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int64_t m = m0 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-        if (m < M) epi(m, n, acc[i][j][r]);
+        const int row = (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+        const int64_t m = m0 + i * 32 + row;
+        const OutT v = (m < M && n < N) ? epi.value(m, n, acc[i][j][r]) : OutT(0);
+        *reinterpret_cast<OutT*>(lds + row * St::kStride + col * (int)sizeof(OutT)) = v;
       }
     }
+    strip_flush<OutT, COLS>(lds, m0 + i * 32, n0, M, N, epi);
   }
 }
 
-// Pair epilogue: blocks 2t (gate) and 2t+1 (up) cover the same 32 output
+// Pair epilogue: blocks 2t (gate) and 2t+1 (up) give the same 32 output
 // columns c0 + 32 t + lane%32.
 template <int TM, int TN, class Acc, class Epi>
 __device__ __forceinline__ void epilogue_pair(const Acc (&acc)[TM][TN], int64_t m0, int64_t c0,
-                                              int64_t M, int64_t NC, const Epi& epi) {
+                                              int64_t M, int64_t NC, const Epi& epi, uint8_t* lds) {
+  using OutT = typename Epi::OutT;
+  constexpr int COLS = TN / 2 * 32;
+  using St = Strip<OutT, COLS>;
   const int lane = threadIdx.x & 63;
 #pragma unroll
-  for (int t = 0; t < TN / 2; ++t) {
-    const int64_t col = c0 + t * 32 + (lane & 31);
-    if (col >= NC) continue;
+  for (int i = 0; i < TM; ++i) {
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
+    for (int t = 0; t < TN / 2; ++t) {
+      const int colw = t * 32 + (lane & 31);
+      const int64_t col = c0 + colw;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int64_t m = m0 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-        if (m < M) epi.pair(m, col, acc[i][2 * t][r], acc[i][2 * t + 1][r]);
+        const int row = (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+        const int64_t m = m0 + i * 32 + row;
+        const OutT v = (m < M && col < NC) ? epi.pair(m, col, acc[i][2 * t][r], acc[i][2 * t + 1][r]) : OutT(0);
+        *reinterpret_cast<OutT*>(lds + row * St::kStride + colw * (int)sizeof(OutT)) = v;
       }
     }
+    strip_flush<OutT, COLS>(lds, m0 + i * 32, c0, M, NC, epi);
   }
 }
 
 // --------------------------------------------------------- main kernel ---
 struct GemmShape {
   int64_t M, N, K;          // N = output columns (pair kernels: 2 * N_out)
-  int64_t a_kbytes;         // K * sizeof(A element)
-  int64_t b_kbytes;         // K * sizeof(B element in global memory)
   int tiles_m, tiles_n;
 };
 
-// One K stage of MFMAs on LDS buffer `sm` for this wave's sub-tile.
-template <class Mma, int BM, int TM, int TN>
-__device__ __forceinline__ void mma_stage(const uint8_t* sm, typename Mma::Acc (&acc)[TM][TN],
-                                          int wm, int wn) {
-  constexpr int KC = Mma::kChunks;
-  constexpr int KSTEPS = 8 / (2 * KC);
-  const int lane = threadIdx.x & 63;
-  const int lr = lane & 31;
-  const int half = lane >> 5;
-  const uint8_t* sa = sm;
-  const uint8_t* sb = sm + BM * kRowBytes;
-#pragma unroll
-  for (int s = 0; s < KSTEPS; ++s) {
-    i32x4 af[TM][KC], bf[TN][KC];
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      const int r = wm * (TM * 32) + i * 32 + lr;
-#pragma unroll
-      for (int u = 0; u < KC; ++u) {
-        const int c = s * 2 * KC + half * KC + u;
-        af[i][u] = *reinterpret_cast<const i32x4*>(sa + r * kRowBytes + swz_chunk(r, c) * 16);
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int r = wn * (TN * 32) + j * 32 + lr;
-#pragma unroll
-      for (int u = 0; u < KC; ++u) {
-        const int c = s * 2 * KC + half * KC + u;
-        bf[j][u] = *reinterpret_cast<const i32x4*>(sb + r * kRowBytes + swz_chunk(r, c) * 16);
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j) acc[i][j] = Mma::mma(af[i], bf[j], acc[i][j]);
-  }
+// Operand sources: base pointers and strides; each workgroup derives its
+// tile's buffer resources from them.
+struct Src2 {
+  const uint8_t* p0; const uint8_t* p1;   // p1: second matrix of a pair (up rows), else = p0
+  int64_t ld_bytes; int64_t rows;          // rows of each matrix
+};
+
+// Wait until at most N vector-memory operations of this wave are in flight.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
 // PAIR = false: plain GEMM, epilogue(m, n, acc).
 // PAIR = true : gate/up pair, epilogue.pair(m, col, acc_gate, acc_up).
-template <class Mma, int BM, int BN, class LoadA, class SrcA, class LoadB, class SrcB,
-          class BStoreArg, bool PAIR, class Epi>
-__global__ void __launch_bounds__(kThreads)
-gemm_tile_kernel(GemmShape sh, SrcA srca, SrcB srcb, BStoreArg barg, Epi epi) {
-  constexpr int TM = BM / 64, TN = BN / 64;    // 32x32 blocks per wave (2x2 waves)
+// b_scale: W8A16 per-tensor weight scale (device pointer) or null.
+template <class Op, int BM, int BN, int WM, int WN, int NBUF, bool PAIR, class Epi>
+__global__ void __launch_bounds__(64 * WM * WN)
+gemm_tile_kernel(GemmShape sh, Src2 sa, Src2 sb, const float* b_scale, Epi epi) {
+  constexpr int NT = 64 * WM * WN;
+  constexpr int TM = BM / WM / 32, TN = BN / WN / 32;   // 32x32 MFMA blocks per wave
+  static_assert(TM >= 1 && TN >= 1 && TM * WM * 32 == BM && TN * WN * 32 == BN, "bad wave tiling");
   static_assert(!PAIR || (TN % 2 == 0), "pair tiles need whole gate/up block pairs");
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2][(BM + BN) * kRowBytes];
+  constexpr int SA = Op::SA, SB = Op::SB;
+  constexpr int STAGE = BM * SA + BN * SB;
+  static_assert(NBUF >= 2 && NBUF * STAGE <= 160 * 1024, "LDS ring exceeds 160 KB");
+  using LA = DirectLoad<BM, SA, NT, false>;
+  using LB = DirectLoad<BN, SB, NT, PAIR>;
+  constexpr int kPerStage = LA::kInstr + LB::kInstr;     // copies per wave per stage
+  static_assert((NBUF - 1) * kPerStage < 64, "too many copies in flight for vmcnt");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[NBUF * STAGE];
 
   const TileCoord tc = tile_of(blockIdx.x, gridDim.x, sh.tiles_m, sh.tiles_n);
   const Epi ep = epi.prepare();
-  const BStoreArg bst = barg.prepare();
   const int64_t m0 = (int64_t)tc.tm * BM;
   const int64_t n0 = (int64_t)tc.tn * BN;
   const int wave = threadIdx.x >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WN, wn = wave % WN;
 
-  typename Mma::Acc acc[TM][TN];
+  LA la;
+  LB lb;
+  la.init(sa.ld_bytes);
+  lb.init(sb.ld_bytes);
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(sa.p0 + m0 * sa.ld_bytes, (sa.rows - m0) * sa.ld_bytes);
+  const int64_t brow0 = PAIR ? (n0 >> 1) : n0;     // pair: both matrices start at column n0/2
+  const int64_t bleft = (sb.rows - brow0) * sb.ld_bytes;
+  const __amdgpu_buffer_rsrc_t rb0 = make_rsrc(sb.p0 + brow0 * sb.ld_bytes, bleft);
+  const __amdgpu_buffer_rsrc_t rb1 = PAIR ? make_rsrc(sb.p1 + brow0 * sb.ld_bytes, bleft) : rb0;
+  const float ws = Op::prep_scale(b_scale);
+
+  typename Op::Acc acc[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -337,66 +458,76 @@ gemm_tile_kernel(GemmShape sh, SrcA srca, SrcB srcb, BStoreArg barg, Epi epi) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
 
-  // stage geometry: 128 bytes of A per row per stage; B advances by the same
-  // number of K elements (its global bytes per stage may differ: fp8 weights
-  // under bf16 activations advance 64 bytes).
-  constexpr int64_t kAStage = kRowBytes;
-  const int64_t b_stage = sh.b_kbytes == sh.a_kbytes ? kRowBytes : kRowBytes / 2;
-  const int nst = (int)((sh.a_kbytes + kAStage - 1) / kAStage);
+  const int a_kb = (int)(sh.K * (SA / kStageK)), b_kb = (int)(sh.K * (SB / kStageK));
+  const int nst = (int)((sh.K + kStageK - 1) / kStageK);
 
-  LoadA la;
-  LoadB lb;
-  const int64_t bn0 = n0;   // B row origin (pair sources interpret it in doubled-N space)
-  la.load(srca, m0, 0, sh.a_kbytes);
-  lb.load(srcb, bn0, 0, sh.b_kbytes);
-  la.store(smem[0]);
-  bst.store(lb, smem[0] + BM * kRowBytes);
+  // prologue: stages 0 .. NBUF-1 in flight, stage 0 complete and visible
+#pragma unroll
+  for (int p = 0; p < NBUF; ++p) {
+    uint8_t* buf = smem + p * STAGE;
+    la.issue(ra, ra, buf, p * SA, a_kb);
+    lb.issue(rb0, rb1, buf + BM * SA, p * SB, b_kb);
+  }
+  wait_vm<(NBUF - 1) * kPerStage>();
   __syncthreads();
 
-  for (int st = 0; st < nst; ++st) {
-    const int cur = st & 1;
-    const bool more = st + 1 < nst;
-    if (more) {
-      la.load(srca, m0, (int64_t)(st + 1) * kAStage, sh.a_kbytes);
-      lb.load(srcb, bn0, (int64_t)(st + 1) * b_stage, sh.b_kbytes);
+  // K-step pipeline: the fragments of the next step are read while the
+  // current step multiplies. The stage barrier sits before the last step of
+  // each stage, whose fragments are already in registers: after it the
+  // next stage is visible (its first fragments load under the last step's
+  // MFMAs) and the stage just read is free to refill.
+  const int ra0 = wm * (TM * 32), rb0i = wn * (TN * 32);
+  using Frag = typename Op::template Frag<TM, TN>;
+  Frag fr[2];
+  Op::template frags<TM, TN>(fr[0], smem, smem + BM * SA, ra0, rb0i, 0);
+  constexpr int S = Op::S;
+  // One stage; P = parity of the stage's first K step in the global step
+  // sequence (so the fragment double buffer is indexed statically).
+  auto run_stage = [&](int st, auto Pc) {
+    constexpr int P = decltype(Pc)::value;
+    const uint8_t* cur = smem + (st % NBUF) * STAGE;
+    const uint8_t* nxt = smem + ((st + 1) % NBUF) * STAGE;
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      if (s == S - 1) {
+        wait_vm<(NBUF - 2) * kPerStage>();     // this wave's copies of stage st+1 landed
+        __syncthreads();                       // ... and every wave's; stage st fully read
+        const int ps = st + NBUF;              // refill stage st's buffer (past K: zeros)
+        uint8_t* buf = smem + (st % NBUF) * STAGE;
+        la.issue(ra, ra, buf, ps * SA, a_kb);
+        lb.issue(rb0, rb1, buf + BM * SA, ps * SB, b_kb);
+        Op::template frags<TM, TN>(fr[(P + s + 1) & 1], nxt, nxt + BM * SA, ra0, rb0i, 0);
+      } else {
+        Op::template frags<TM, TN>(fr[(P + s + 1) & 1], cur, cur + BM * SA, ra0, rb0i, s + 1);
+      }
+      Op::template mma<TM, TN>(fr[(P + s) & 1], acc, ws);
     }
-    mma_stage<Mma, BM, TM, TN>(smem[cur], acc, wm, wn);
-    if (more) {
-      la.store(smem[cur ^ 1]);
-      bst.store(lb, smem[cur ^ 1] + BM * kRowBytes);
+  };
+  if constexpr (S % 2 == 0) {
+    for (int st = 0; st < nst; ++st) run_stage(st, std::integral_constant<int, 0>{});
+  } else {
+    int st = 0;
+    for (; st + 1 < nst; st += 2) {
+      run_stage(st, std::integral_constant<int, 0>{});
+      run_stage(st + 1, std::integral_constant<int, 1>{});
     }
-    __syncthreads();
+    if (st < nst) run_stage(st, std::integral_constant<int, 0>{});
   }
+  wait_vm<0>();    // past-K copies still land in the ring; drain before reusing LDS
+  __syncthreads();
 
+  // per-wave output strips in the (now idle) ring
+  using OutT = typename Epi::OutT;
+  constexpr int kStripBytes = Strip<OutT, (PAIR ? TN / 2 : TN) * 32>::kBytes;
+  static_assert(kStripBytes * WM * WN <= NBUF * STAGE, "output strips exceed the LDS ring");
+  uint8_t* strip = smem + wave * kStripBytes;
   const int64_t wm0 = m0 + wm * (TM * 32);
   if constexpr (PAIR) {
     const int64_t c0 = (n0 >> 1) + wn * (TN * 16);
-    epilogue_pair<TM, TN>(acc, wm0, c0, sh.M, sh.N >> 1, ep);
+    epilogue_pair<TM, TN>(acc, wm0, c0, sh.M, sh.N >> 1, ep, strip);
   } else {
-    epilogue_single<TM, TN>(acc, wm0, n0 + wn * (TN * 32), sh.M, sh.N, ep);
+    epilogue_single<TM, TN>(acc, wm0, n0 + wn * (TN * 32), sh.M, sh.N, ep, strip);
   }
 }
-
-// B-stage store adaptors: plain copy, or dequantizing fp8 -> half types.
-struct BStorePlain {
-  __device__ __forceinline__ BStorePlain prepare() const { return *this; }
-  template <class L>
-  __device__ __forceinline__ void store(const L& l, uint8_t* lds) const { l.store(lds); }
-};
-// The per-tensor weight scale lives in device memory (a [1] fp32 tensor);
-// it is read once per workgroup and rounded to the activation type, as
-// scale.to(T) does in the kitchen dequant formula.
-template <bool BF16>
-struct BStoreDequant {
-  const float* sp; float s;
-  __device__ __forceinline__ BStoreDequant prepare() const {
-    BStoreDequant r = *this;
-    if (sp) r.s = BF16 ? bf16_f32(bf16_rte(sp[0])) : f16_f32(f16_rte(sp[0]));
-    else r.s = 1.0f;
-    return r;
-  }
-  template <class L>
-  __device__ __forceinline__ void store(const L& l, uint8_t* lds) const { l.store(lds, s); }
-};
 
 }  // namespace c4q

@@ -65,7 +65,7 @@ gemm_generic_kernel(int64_t M, int64_t N, int64_t K, int64_t nbx, Op op, Epi epi
   const Epi ep = epi.prepare();
   typename Op::Acc acc = 0;
   for (int64_t k = 0; k < K; ++k) acc = acc + op.av(m, k) * op.bv(n, k);
-  ep(m, n, acc);
+  ep.put(m, n, ep.value(m, n, acc));
 }
 
 // FFN pair fallback: gate/up accumulators for output column `col`.
@@ -84,7 +84,7 @@ pair_generic_kernel(int64_t M, int64_t NC, int64_t K, int64_t nbx, const int8_t*
     ag += x * (int32_t)g[col * ldw + k];
     au += x * (int32_t)u[col * ldw + k];
   }
-  ep.pair(m, col, ag, au);
+  ep.put(m, col, ep.pair(m, col, ag, au));
 }
 
 }  // namespace c4q

@@ -28,8 +28,8 @@ extern "C" int c4q_i8_gemm_nt_i32(const int8_t* a, int64_t lda, const int8_t* b,
   const char* what = "c4q_i8_gemm_nt_i32";
   int st = check_i8_args(a, lda, b, ldb, c, ldc, M, N, K, what);
   if (st) return st;
-  EpiI32 epi{c, ldc};
-  return run_gemm8<MmaI8, GenI8>(reinterpret_cast<const uint8_t*>(a), lda,
+  EpiI32 epi{{c, ldc, rows_vec16(c, ldc, 4)}};
+  return run_gemm8<OpI8, GenI8>(reinterpret_cast<const uint8_t*>(a), lda,
                                  reinterpret_cast<const uint8_t*>(b), ldb, M, N, K, epi,
                                  as_stream(stream), what);
 }
@@ -42,8 +42,8 @@ extern "C" int c4q_i8_gemm_nt_fused(const int8_t* a, int64_t lda, const int8_t* 
   int st = check_i8_args(a, lda, b, ldb, d, ldd, M, N, K, what);
   if (st) return st;
   C4Q_REQUIRE(M == 0 || N == 0 || row_scale != nullptr, C4Q_ERR_ARG, "%s: null row_scale", what);
-  EpiRowScale epi{d, ldd, row_scale, bias};
-  return run_gemm8<MmaI8, GenI8>(reinterpret_cast<const uint8_t*>(a), lda,
+  EpiRowScale epi{{d, ldd, rows_vec16(d, ldd, 2)}, row_scale, bias};
+  return run_gemm8<OpI8, GenI8>(reinterpret_cast<const uint8_t*>(a), lda,
                                  reinterpret_cast<const uint8_t*>(b), ldb, M, N, K, epi,
                                  as_stream(stream), what);
 }
@@ -57,8 +57,8 @@ extern "C" int c4q_i8_gemm_nt_fused_cs(const int8_t* a, int64_t lda, const int8_
   if (st) return st;
   C4Q_REQUIRE(M == 0 || N == 0 || (row_scale != nullptr && col_scale != nullptr), C4Q_ERR_ARG,
               "%s: null row_scale/col_scale", what);
-  EpiRowColScale epi{d, ldd, row_scale, col_scale, bias};
-  return run_gemm8<MmaI8, GenI8>(reinterpret_cast<const uint8_t*>(a), lda,
+  EpiRowColScale epi{{d, ldd, rows_vec16(d, ldd, 2)}, row_scale, col_scale, bias};
+  return run_gemm8<OpI8, GenI8>(reinterpret_cast<const uint8_t*>(a), lda,
                                  reinterpret_cast<const uint8_t*>(b), ldb, M, N, K, epi,
                                  as_stream(stream), what);
 }
@@ -76,9 +76,9 @@ extern "C" int c4q_i8_ffn_pair(const int8_t* a, int64_t lda, const int8_t* w_gat
   C4Q_REQUIRE(K == 0 || w_up != nullptr, C4Q_ERR_ARG, "%s: null w_up", what);
   C4Q_REQUIRE(row_scale && gate_scale && up_scale, C4Q_ERR_ARG, "%s: null scale", what);
   hipStream_t s = as_stream(stream);
-  EpiPair epi{d, ldd, row_scale, gate_scale, up_scale, table_gate, table_up};
+  EpiPair epi{{d, ldd, rows_vec16(d, ldd, 2)}, row_scale, gate_scale, up_scale, table_gate, table_up};
   const bool tiled = K > 0 && K % 16 == 0 && aligned16(a) && aligned16(w_gate) &&
-                     aligned16(w_up) && lda % 16 == 0 && ldw % 16 == 0;
+                     aligned16(w_up) && lda % 16 == 0 && ldw % 16 == 0 && tile_offsets_fit(lda, ldw);
   if (!tiled) {
     const int64_t nbx = cdiv(N_out, 64);
     const int64_t blocks = nbx * cdiv(M, 4);
@@ -87,22 +87,12 @@ extern "C" int c4q_i8_ffn_pair(const int8_t* a, int64_t lda, const int8_t* w_gat
                        N_out, K, nbx, a, lda, w_gate, w_up, ldw, epi);
     return check_launch(what);
   }
-  GemmShape sh{M, 2 * N_out, K, K, K, 0, 0};
-  RowsPlain ra{reinterpret_cast<const uint8_t*>(a), lda, M};
-  RowsPair rb{reinterpret_cast<const uint8_t*>(w_gate), reinterpret_cast<const uint8_t*>(w_up),
-              ldw, N_out};
-  switch (pick_tile(M, 2 * N_out)) {
-    case TILE_256x256:
-      return launch_tile<MmaI8, 256, 256, Load8<256, RowsPlain>, RowsPlain, Load8<256, RowsPair>,
-                         RowsPair, BStorePlain, true>(sh, 2 * N_out, ra, rb, BStorePlain{}, epi, s,
-                                                      what);
-    case TILE_128x128:
-      return launch_tile<MmaI8, 128, 128, Load8<128, RowsPlain>, RowsPlain, Load8<128, RowsPair>,
-                         RowsPair, BStorePlain, true>(sh, 2 * N_out, ra, rb, BStorePlain{}, epi, s,
-                                                      what);
-    default:
-      return launch_tile<MmaI8, 64, 128, Load8<64, RowsPlain>, RowsPlain, Load8<128, RowsPair>,
-                         RowsPair, BStorePlain, true>(sh, 2 * N_out, ra, rb, BStorePlain{}, epi, s,
-                                                      what);
-  }
+  GemmShape sh{M, 2 * N_out, K, 0, 0};
+  const Src2 sa{reinterpret_cast<const uint8_t*>(a), reinterpret_cast<const uint8_t*>(a), lda, M};
+  const Src2 sb{reinterpret_cast<const uint8_t*>(w_gate), reinterpret_cast<const uint8_t*>(w_up),
+                ldw, N_out};
+  return with_tile(pick_tile(M, 2 * N_out), [&](auto t) {
+    using T = decltype(t);
+    return launch_tile<T, OpI8, true>(sh, 2 * N_out, sa, sb, nullptr, epi, s, what);
+  });
 }

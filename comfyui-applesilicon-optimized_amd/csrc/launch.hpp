@@ -1,5 +1,7 @@
 // Launch helpers binding the tiled and generic kernels to an entry point.
 #pragma once
+#include <stdlib.h>
+
 #include "api_common.hpp"
 #include "epilogues.hpp"
 #include "gemm_tile.hpp"
@@ -7,17 +9,62 @@
 
 namespace c4q {
 
-template <class Mma, int BM, int BN, class LoadA, class SrcA, class LoadB, class SrcB, class BSt,
-          bool PAIR, class Epi>
-int launch_tile(GemmShape sh, int64_t n_rows_b, const SrcA& sa, const SrcB& sb, const BSt& bst,
+// Tile variants of the MFMA kernels: BM x BN output tile, WM x WN waves,
+// and the LDS budget of one workgroup (160 KB: one workgroup per CU; less
+// leaves room for two or three).
+template <int BM_, int BN_, int WM_, int WN_, int LDS_KB_>
+struct Tile {
+  static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, NT = 64 * WM_ * WN_;
+  static constexpr int LDS = LDS_KB_ * 1024;
+};
+
+// Ring depth: as many 64-K stages as the budget holds, at most 4.
+template <class T, class Op>
+constexpr int ring_depth() {
+  constexpr int stage = T::BM * Op::SA + T::BN * Op::SB;
+  constexpr int n = T::LDS / stage;
+  return n > 4 ? 4 : (n < 2 ? 2 : n);
+}
+enum TileId : int {
+  TILE_256x256_W8 = 0,   // 8 waves (2 per SIMD), 128x64 per wave
+  TILE_256x256_W4 = 1,   // 4 waves, 128x128 per wave
+  TILE_128x128_W4 = 2,   // 4 waves, 64x64 per wave
+  TILE_64x128_W4 = 3,    // 4 waves, 32x64 per wave
+  TILE_COUNT = 4,
+};
+
+template <class F>
+int with_tile(int id, F&& f) {
+  switch (id) {
+    case TILE_256x256_W8: return f(Tile<256, 256, 2, 4, 160>{});
+    case TILE_256x256_W4: return f(Tile<256, 256, 2, 2, 160>{});
+    case TILE_128x128_W4: return f(Tile<128, 128, 2, 2, 80>{});
+    default: return f(Tile<64, 128, 2, 2, 53>{});
+  }
+}
+
+// Tile choice: the largest tile that still gives every CU work. A tile id in
+// the environment variable C4Q_TILE (0..3) overrides it, for tuning sweeps.
+inline int pick_tile(int64_t M, int64_t N) {
+  const char* env = getenv("C4Q_TILE");
+  if (env && env[0] >= '0' && env[0] < '0' + TILE_COUNT && env[1] == 0) return env[0] - '0';
+  const int64_t cus = 256;
+  if (cdiv(M, 256) * cdiv(N, 256) >= 2 * cus) return TILE_256x256_W8;
+  if (cdiv(M, 128) * cdiv(N, 128) >= cus) return TILE_128x128_W4;
+  return TILE_64x128_W4;
+}
+
+template <class T, class Op, bool PAIR, class Epi>
+int launch_tile(GemmShape sh, int64_t n_rows_b, const Src2& sa, const Src2& sb, const float* b_scale,
                 const Epi& epi, hipStream_t s, const char* what) {
-  sh.tiles_m = (int)cdiv(sh.M, BM);
-  sh.tiles_n = (int)cdiv(n_rows_b, BN);
+  sh.tiles_m = (int)cdiv(sh.M, T::BM);
+  sh.tiles_n = (int)cdiv(n_rows_b, T::BN);
   const int64_t blocks = (int64_t)sh.tiles_m * sh.tiles_n;
   C4Q_REQUIRE(blocks < (1ll << 31), C4Q_ERR_SHAPE, "%s: problem too large (%lld tiles)", what,
               (long long)blocks);
-  hipLaunchKernelGGL((gemm_tile_kernel<Mma, BM, BN, LoadA, SrcA, LoadB, SrcB, BSt, PAIR, Epi>),
-                     dim3((unsigned)blocks), dim3(kThreads), 0, s, sh, sa, sb, bst, epi);
+  constexpr int nbuf = ring_depth<T, Op>();
+  hipLaunchKernelGGL((gemm_tile_kernel<Op, T::BM, T::BN, T::WM, T::WN, nbuf, PAIR, Epi>),
+                     dim3((unsigned)blocks), dim3(T::NT), 0, s, sh, sa, sb, b_scale, epi);
   return check_launch(what);
 }
 
@@ -32,29 +79,26 @@ int launch_generic(int64_t M, int64_t N, int64_t K, const Op& op, const Epi& epi
   return check_launch(what);
 }
 
+// The tiled kernels address one tile (at most 256 rows) with 32-bit byte
+// offsets inside a buffer resource.
+inline bool tile_offsets_fit(int64_t lda_bytes, int64_t ldb_bytes) {
+  return lda_bytes <= (1ll << 22) && ldb_bytes <= (1ll << 22);
+}
+
 // 8-bit x 8-bit GEMM (int8 or fp8 operands) with epilogue Epi.
-template <class Mma, class GenOp, class Epi>
+template <class Op, class GenOp, class Epi>
 int run_gemm8(const uint8_t* a, int64_t lda, const uint8_t* b, int64_t ldb, int64_t M, int64_t N,
               int64_t K, const Epi& epi, hipStream_t s, const char* what) {
   if (M == 0 || N == 0) return C4Q_OK;
   const bool tiled = K > 0 && K % 16 == 0 && aligned16(a) && aligned16(b) && lda % 16 == 0 &&
-                     ldb % 16 == 0;
-  if (!tiled) {
-    return launch_generic(M, N, K, GenOp::make(a, lda, b, ldb), epi, s, what);
-  }
-  GemmShape sh{M, N, K, K, K, 0, 0};
-  RowsPlain ra{a, lda, M}, rb{b, ldb, N};
-  switch (pick_tile(M, N)) {
-    case TILE_256x256:
-      return launch_tile<Mma, 256, 256, Load8<256, RowsPlain>, RowsPlain, Load8<256, RowsPlain>,
-                         RowsPlain, BStorePlain, false>(sh, N, ra, rb, BStorePlain{}, epi, s, what);
-    case TILE_128x128:
-      return launch_tile<Mma, 128, 128, Load8<128, RowsPlain>, RowsPlain, Load8<128, RowsPlain>,
-                         RowsPlain, BStorePlain, false>(sh, N, ra, rb, BStorePlain{}, epi, s, what);
-    default:
-      return launch_tile<Mma, 64, 128, Load8<64, RowsPlain>, RowsPlain, Load8<128, RowsPlain>,
-                         RowsPlain, BStorePlain, false>(sh, N, ra, rb, BStorePlain{}, epi, s, what);
-  }
+                     ldb % 16 == 0 && tile_offsets_fit(lda, ldb);
+  if (!tiled) return launch_generic(M, N, K, GenOp::make(a, lda, b, ldb), epi, s, what);
+  GemmShape sh{M, N, K, 0, 0};
+  const Src2 sa{a, a, lda, M}, sb{b, b, ldb, N};
+  return with_tile(pick_tile(M, N), [&](auto t) {
+    using T = decltype(t);
+    return launch_tile<T, Op, false>(sh, N, sa, sb, nullptr, epi, s, what);
+  });
 }
 
 }  // namespace c4q

@@ -311,3 +311,43 @@ def test_moss_pair_exact(dev):
                        tg.to(dev))
     ref = op.moss_pair(q.numpy(), w.numpy(), rs.numpy(), cs.numpy(), *oact.situ_tables())
     assert_bits_equal(bits16(out), ref, "moss pair")
+
+
+# ---------------------------------------------------- every tile variant ---
+
+@pytest.mark.parametrize("tile", ["0", "1", "2", "3"])
+def test_every_tile_variant(dev, monkeypatch, tile):
+    """Force each MFMA tile variant (C4Q_TILE) on ragged shapes: INT8 fused
+    epilogue and pair bit-exact, fp8 / W8A16 within tolerance."""
+    monkeypatch.setenv("C4Q_TILE", tile)
+    g = gen(100 + int(tile))
+    M, K, N = 300, 1040, 520          # ragged M and N tails, K tail inside a 128-byte stage
+    a, b = _randint8((M, K), g), _randint8((N, K), g)
+    rs = torch.rand(M, generator=g) * 0.01
+    cs = torch.rand(N, generator=g) * 0.02
+    bb = torch.randn(N, generator=g).to(torch.bfloat16)
+    c = ops.i8_matmul2d_nt(a.to(dev), b.to(dev))
+    ref_c = oi.i8_matmul2d_nt(a.numpy(), b.numpy())
+    assert_bits_equal(c.cpu().numpy(), ref_c, f"tile {tile} int32")
+    d = ops.i8_matmul2d_nt_fused_cs(a.to(dev), b.to(dev), rs.to(dev), cs.to(dev), bb.to(dev))
+    assert_bits_equal(bits16(d), oi.epilogue_rowcolscale(ref_c, rs.numpy(), cs.numpy(), bits16(bb)),
+                      f"tile {tile} fused_cs")
+    wu = _randint8((N, K), g)
+    us = torch.rand(N, generator=g) * 0.02
+    silu = torch.from_numpy(oact.silu_table().view(np.int16))
+    p = ops.ffn_pair(a.to(dev), b.to(dev), wu.to(dev), rs.to(dev), cs.to(dev), us.to(dev),
+                     silu.to(dev), None)
+    assert_bits_equal(bits16(p), op.krea2_pair(a.numpy(), b.numpy(), wu.numpy(), rs.numpy(),
+                                               cs.numpy(), us.numpy()), f"tile {tile} pair")
+    af = _fp8(torch.randn(M, K, generator=g))
+    wf = _fp8(torch.randn(N, K, generator=g) * 0.1)
+    sa, sb = torch.tensor(0.7), torch.tensor(1.3)
+    o = ops.scaled_mm(af.to(dev), wf.to(dev).t(), out_dtype=torch.bfloat16, scale_a=sa.to(dev),
+                      scale_b=sb.to(dev))
+    ref = of.scaled_mm(u8(af), u8(wf), sa.numpy(), sb.numpy())
+    assert_close(bf16_to_f32(bits16(o)), bf16_to_f32(ref), f"tile {tile} fp8")
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    ws = (wf.float().abs().amax() / 448).reshape(1)
+    y = ops.w8a16_linear(x.to(dev), wf.to(dev), ws.to(dev), bb.to(dev))
+    ref = of.w8a16_linear(bits16(x), u8(wf), ws.numpy(), bits16(bb))
+    assert_close(bf16_to_f32(bits16(y)), bf16_to_f32(ref), f"tile {tile} w8a16")
