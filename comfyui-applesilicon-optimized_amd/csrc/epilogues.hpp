@@ -1,18 +1,24 @@
-// Epilogue functors: turn one accumulator into one output element.
+// Epilogue functors: turn accumulators into stored output elements.
 //
-// Every rounding step is explicit (bf16_rte / f16_rte from numerics.hpp) and
-// the library is compiled with -ffp-contract=off, so each multiply and add
-// below rounds exactly once, in the order written. That order is the
-// reference's; the citation sits on each functor.
+// Every rounding step is explicit and the library is compiled with
+// -ffp-contract=off, so each multiply and add below rounds exactly once, in
+// the order written. That order is the reference's; the citation sits on
+// each functor.
 //
 // Interface (used by the tiled kernels' staged store and by the generic
 // kernels):
-//   OutT                      stored element type (16- or 32-bit bits)
-//   prepare()                 per-workgroup copy with scalars loaded
-//   value(m, n, acc)          the output bits of element (m, n)
-//   pair(m, col, a1, a2)      (pair epilogues) the output of column col
-//   row(m)                    byte pointer to output row m
-//   vec                       rows are 16-byte aligned: chunked stores allowed
+//   OutT                       stored element type (16- or 32-bit bits)
+//   prepare()                  per-workgroup copy with scalars loaded
+//   value4(m, n, v, nv)        packed outputs of elements (m, n .. n+3) from
+//                              accumulators v[0..3]; only the first nv are
+//                              valid (the rest are never read or stored)
+//   pair4(m, n, g, u, nv)      (pair epilogues) the same from gate/up sums
+//   row(m), vec                byte pointer to output row m; rows are
+//                              16-byte aligned (chunked stores allowed)
+//
+// Neutral elements keep absent terms branch-free and exact: an absent scale
+// multiplies by 1.0f (x * 1 == x for every x), an absent bias adds -0.0f
+// (x + -0 == x for every x, -0 included).
 #pragma once
 #include <type_traits>
 
@@ -23,6 +29,26 @@ namespace c4q {
 enum : int { DT_BF16 = 0, DT_F16 = 1, DT_F32 = 2 };
 enum : int { SC_NONE = 0, SC_TENSOR = 1, SC_VECTOR = 2 };
 
+typedef __bf16 epi_bf16x2 __attribute__((ext_vector_type(2)));
+
+// Two floats to packed bf16 with one v_cvt_pk_bf16_f32 (round to nearest
+// even): bit-identical to bf16_rte for every non-NaN float (all 2^32 inputs
+// are compared on the GPU in tests/test_gpu_numerics.py).
+__device__ __forceinline__ uint32_t bf16x2_rne(float lo, float hi) {
+  const epi_bf16x2 h = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, h);
+}
+// Two floats to packed IEEE half, round to nearest even (v_cvt_f16_f32;
+// checked the same way against f16_rte).
+__device__ __forceinline__ uint32_t f16x2_rne(float lo, float hi) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)lo) |
+         ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)hi) << 16);
+}
+__device__ __forceinline__ float bf16lo(uint32_t p) { return bits_f32(p << 16); }
+__device__ __forceinline__ float bf16hi(uint32_t p) { return bits_f32(p & 0xFFFF0000u); }
+
+__device__ const float kOneF = 1.0f;     // target of absent-scale pointers
+
 __device__ __forceinline__ float load_f32(const void* p, int dt, int64_t i) {
   if (dt == DT_BF16) return bf16_f32(static_cast<const uint16_t*>(p)[i]);
   if (dt == DT_F16) return f16_f32(static_cast<const uint16_t*>(p)[i]);
@@ -32,20 +58,29 @@ __device__ __forceinline__ float load_f32(const void* p, int dt, int64_t i) {
 template <class T>
 struct EpiOut {
   using OutT = T;
+  using Packed = typename std::conditional<sizeof(T) == 2, uint2, uint4>::type;
   void* d; int64_t ldd; int vec;
   __device__ __forceinline__ uint8_t* row(int64_t m) const {
     return static_cast<uint8_t*>(d) + m * ldd * (int64_t)sizeof(T);
   }
-  __device__ __forceinline__ void put(int64_t m, int64_t n, T v) const {
-    reinterpret_cast<T*>(row(m))[n] = v;
-  }
 };
+
+// Column index for parameter loads of element q of a group: past-the-end
+// columns read column n instead (their results are discarded).
+__device__ __forceinline__ int64_t colq(int64_t n, int q, int nv) { return q < nv ? n + q : n; }
+
+template <class Packed>
+__device__ __forceinline__ Packed pack_bf16x4(float a, float b, float c, float d) {
+  return Packed{bf16x2_rne(a, b), bf16x2_rne(c, d)};
+}
 
 // Raw INT32 store: torch._int_mm / i8_matmul2d_nt
 // (reference _patches/int8_ext/int8_gemm.mm:81-94).
 struct EpiI32 : EpiOut<uint32_t> {
   __device__ __forceinline__ EpiI32 prepare() const { return *this; }
-  __device__ __forceinline__ uint32_t value(int64_t, int64_t, int32_t v) const { return (uint32_t)v; }
+  __device__ __forceinline__ uint4 value4(int64_t, int64_t, const int32_t (&v)[4], int) const {
+    return uint4{(uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]};
+  }
 };
 
 // Per-tensor fused dequant: D = bf16(f32(C) * row_scale[m]), then optional
@@ -54,10 +89,17 @@ struct EpiI32 : EpiOut<uint32_t> {
 struct EpiRowScale : EpiOut<uint16_t> {
   const float* rs; const uint16_t* bias;
   __device__ __forceinline__ EpiRowScale prepare() const { return *this; }
-  __device__ __forceinline__ uint16_t value(int64_t m, int64_t n, int32_t v) const {
-    uint16_t h = bf16_rte((float)v * rs[m]);
-    if (bias) h = bf16_rte(bf16_f32(h) + bf16_f32(bias[n]));
-    return h;
+  __device__ __forceinline__ uint2 value4(int64_t m, int64_t n, const int32_t (&v)[4], int nv) const {
+    const float r = rs[m];
+    uint2 p = pack_bf16x4<uint2>((float)v[0] * r, (float)v[1] * r, (float)v[2] * r, (float)v[3] * r);
+    if (bias) {
+      float b[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) b[q] = bf16_f32(bias[colq(n, q, nv)]);
+      p = pack_bf16x4<uint2>(bf16lo(p.x) + b[0], bf16hi(p.x) + b[1], bf16lo(p.y) + b[2],
+                             bf16hi(p.y) + b[3]);
+    }
+    return p;
   }
 };
 
@@ -67,11 +109,20 @@ struct EpiRowScale : EpiOut<uint16_t> {
 struct EpiRowColScale : EpiOut<uint16_t> {
   const float* rs; const float* cs; const uint16_t* bias;
   __device__ __forceinline__ EpiRowColScale prepare() const { return *this; }
-  __device__ __forceinline__ uint16_t value(int64_t m, int64_t n, int32_t v) const {
-    const float s = cs[n] * rs[m];
-    uint16_t h = bf16_rte((float)v * s);
-    if (bias) h = bf16_rte(bf16_f32(h) + bf16_f32(bias[n]));
-    return h;
+  __device__ __forceinline__ uint2 value4(int64_t m, int64_t n, const int32_t (&v)[4], int nv) const {
+    const float r = rs[m];
+    float x[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) x[q] = (float)v[q] * (cs[colq(n, q, nv)] * r);
+    uint2 p = pack_bf16x4<uint2>(x[0], x[1], x[2], x[3]);
+    if (bias) {
+      float b[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) b[q] = bf16_f32(bias[colq(n, q, nv)]);
+      p = pack_bf16x4<uint2>(bf16lo(p.x) + b[0], bf16hi(p.x) + b[1], bf16lo(p.y) + b[2],
+                             bf16hi(p.y) + b[3]);
+    }
+    return p;
   }
 };
 
@@ -79,30 +130,41 @@ struct EpiRowColScale : EpiOut<uint16_t> {
 // * scale_b, * scale_result, + f32(bias), each in f32 and in this order,
 // one final rounding to the output dtype
 // (reference _patches/scaled_mm_fp8.py:123-146). F32OUT selects a 32-bit
-// output; otherwise out_dt picks bf16 or f16.
+// output; otherwise out_dt picks bf16 or f16. Scale pointers are read with a
+// stride (0: per tensor, 1: per row / column); an absent scale reads 1.0f.
 template <bool F32OUT>
 struct EpiScaled : EpiOut<typename std::conditional<F32OUT, uint32_t, uint16_t>::type> {
   using Base = EpiOut<typename std::conditional<F32OUT, uint32_t, uint16_t>::type>;
-  using OutT = typename Base::OutT;
+  using Packed = typename Base::Packed;
   int out_dt;
   const float* sa; int sa_mode; const float* sb; int sb_mode; const float* sr;
   const void* bias; int bias_dt;
-  float sa0, sb0, sr0;
+  int sa_step, sb_step;
+  float sr0;
   __device__ __forceinline__ EpiScaled prepare() const {
     EpiScaled e = *this;
-    e.sa0 = sa_mode == SC_TENSOR ? sa[0] : 1.0f;
-    e.sb0 = sb_mode == SC_TENSOR ? sb[0] : 1.0f;
+    if (sa_mode == SC_NONE) e.sa = &kOneF;
+    if (sb_mode == SC_NONE) e.sb = &kOneF;
+    e.sa_step = sa_mode == SC_VECTOR ? 1 : 0;
+    e.sb_step = sb_mode == SC_VECTOR ? 1 : 0;
     e.sr0 = sr ? sr[0] : 1.0f;
     return e;
   }
-  __device__ __forceinline__ OutT value(int64_t m, int64_t n, float v) const {
-    float o = v;
-    if (sa_mode == SC_TENSOR) o = o * sa0; else if (sa_mode == SC_VECTOR) o = o * sa[m];
-    if (sb_mode == SC_TENSOR) o = o * sb0; else if (sb_mode == SC_VECTOR) o = o * sb[n];
-    if (sr) o = o * sr0;
-    if (bias) o = o + load_f32(bias, bias_dt, n);
-    if constexpr (F32OUT) return f32_bits(o);
-    else return out_dt == DT_F16 ? f16_rte(o) : bf16_rte(o);
+  __device__ __forceinline__ Packed value4(int64_t m, int64_t n, const float (&v)[4], int nv) const {
+    const float a = sa[m * sa_step];
+    float o[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) o[q] = ((v[q] * a) * sb[colq(n, q, nv) * sb_step]) * sr0;
+    if (bias) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) o[q] = o[q] + load_f32(bias, bias_dt, colq(n, q, nv));
+    }
+    if constexpr (F32OUT) {
+      return Packed{f32_bits(o[0]), f32_bits(o[1]), f32_bits(o[2]), f32_bits(o[3])};
+    } else {
+      if (out_dt == DT_F16) return Packed{f16x2_rne(o[0], o[1]), f16x2_rne(o[2], o[3])};
+      return pack_bf16x4<Packed>(o[0], o[1], o[2], o[3]);
+    }
   }
 };
 
@@ -114,19 +176,25 @@ struct EpiScaled : EpiOut<typename std::conditional<F32OUT, uint32_t, uint16_t>:
 template <bool F32OUT>
 struct EpiW8A16 : EpiOut<typename std::conditional<F32OUT, uint32_t, uint16_t>::type> {
   using Base = EpiOut<typename std::conditional<F32OUT, uint32_t, uint16_t>::type>;
-  using OutT = typename Base::OutT;
+  using Packed = typename Base::Packed;
   int out_dt; const void* bias; int bias_dt; const uint16_t* act;
   __device__ __forceinline__ EpiW8A16 prepare() const { return *this; }
-  __device__ __forceinline__ OutT value(int64_t, int64_t n, float v) const {
-    float o = v;
-    if (bias) o = o + load_f32(bias, bias_dt, n);
+  __device__ __forceinline__ Packed value4(int64_t, int64_t n, const float (&v)[4], int nv) const {
+    float o[4] = {v[0], v[1], v[2], v[3]};
+    if (bias) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) o[q] = o[q] + load_f32(bias, bias_dt, colq(n, q, nv));
+    }
     if constexpr (F32OUT) {
-      return f32_bits(o);
+      return Packed{f32_bits(o[0]), f32_bits(o[1]), f32_bits(o[2]), f32_bits(o[3])};
     } else {
-      if (out_dt == DT_F16) return f16_rte(o);
-      uint16_t h = bf16_rte(o);
-      if (act) h = act[h];
-      return h;
+      if (out_dt == DT_F16) return Packed{f16x2_rne(o[0], o[1]), f16x2_rne(o[2], o[3])};
+      Packed p = pack_bf16x4<Packed>(o[0], o[1], o[2], o[3]);
+      if (act) {
+        p.x = (uint32_t)act[p.x & 0xFFFFu] | ((uint32_t)act[p.x >> 16] << 16);
+        p.y = (uint32_t)act[p.y & 0xFFFFu] | ((uint32_t)act[p.y >> 16] << 16);
+      }
+      return p;
     }
   }
 };
@@ -142,14 +210,42 @@ struct EpiPair : EpiOut<uint16_t> {
   const float* rs; const float* s1; const float* s2;
   const uint16_t* t1; const uint16_t* t2;
   __device__ __forceinline__ EpiPair prepare() const { return *this; }
-  __device__ __forceinline__ uint16_t pair(int64_t m, int64_t col, int32_t c1, int32_t c2) const {
+  __device__ __forceinline__ uint2 pair4(int64_t m, int64_t n, const int32_t (&g)[4],
+                                         const int32_t (&u)[4], int nv) const {
     const float r = rs[m];
-    uint16_t x1 = bf16_rte((float)c1 * (s1[col] * r));
-    uint16_t x2 = bf16_rte((float)c2 * (s2[col] * r));
-    if (t1) x1 = t1[x1];
-    if (t2) x2 = t2[x2];
-    return bf16_rte(bf16_f32(x1) * bf16_f32(x2));
+    float a[4], b[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int64_t c = colq(n, q, nv);
+      a[q] = (float)g[q] * (s1[c] * r);
+      b[q] = (float)u[q] * (s2[c] * r);
+    }
+    uint2 x1 = pack_bf16x4<uint2>(a[0], a[1], a[2], a[3]);
+    uint2 x2 = pack_bf16x4<uint2>(b[0], b[1], b[2], b[3]);
+    if (t1) {
+      x1.x = (uint32_t)t1[x1.x & 0xFFFFu] | ((uint32_t)t1[x1.x >> 16] << 16);
+      x1.y = (uint32_t)t1[x1.y & 0xFFFFu] | ((uint32_t)t1[x1.y >> 16] << 16);
+    }
+    if (t2) {
+      x2.x = (uint32_t)t2[x2.x & 0xFFFFu] | ((uint32_t)t2[x2.x >> 16] << 16);
+      x2.y = (uint32_t)t2[x2.y & 0xFFFFu] | ((uint32_t)t2[x2.y >> 16] << 16);
+    }
+    return pack_bf16x4<uint2>(bf16lo(x1.x) * bf16lo(x2.x), bf16hi(x1.x) * bf16hi(x2.x),
+                              bf16lo(x1.y) * bf16lo(x2.y), bf16hi(x1.y) * bf16hi(x2.y));
   }
 };
+
+// Store a packed group of 4 outputs at (m, n .. n+nv-1).
+template <class Epi, class Packed>
+__device__ __forceinline__ void store_group(const Epi& epi, int64_t m, int64_t n, int nv, Packed p) {
+  using OutT = typename Epi::OutT;
+  uint8_t* dst = epi.row(m) + n * (int64_t)sizeof(OutT);
+  if (epi.vec && nv == 4) {
+    *reinterpret_cast<Packed*>(dst) = p;
+    return;
+  }
+  const OutT* e = reinterpret_cast<const OutT*>(&p);
+  for (int q = 0; q < nv; ++q) reinterpret_cast<OutT*>(dst)[q] = e[q];
+}
 
 }  // namespace c4q

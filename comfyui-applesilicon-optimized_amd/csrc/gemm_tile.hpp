@@ -16,8 +16,9 @@
 //     hides behind several stages of MFMA work; one barrier per stage;
 //   * inside a stage the LDS fragments of the next K step are read while the
 //     current step multiplies, across stage boundaries too;
-//   * the epilogue stages each wave's output strip through LDS so that
-//     global stores are whole 16-byte chunks of output rows;
+//   * the epilogue stages each wave's accumulators through LDS, then applies
+//     the output arithmetic in a compact loop over 4-column groups and
+//     stores whole 8/16-byte chunks of output rows;
 //   * the copy reads through buffer resources based at the tile origin whose
 //     range ends at the matrix end: tail rows and the K tail read as zero in
 //     hardware (stages past K are issued with out-of-range offsets, so every
@@ -34,6 +35,7 @@
 #pragma once
 #include <type_traits>
 
+#include "epilogues.hpp"
 #include "numerics.hpp"
 
 namespace c4q {
@@ -298,98 +300,99 @@ __device__ __forceinline__ TileCoord tile_of(int bid, int nblocks, int tiles_m, 
 }
 
 // ------------------------------------------------------------ epilogue ---
-// Each wave stores its sub-tile one 32-row strip at a time through a
-// private LDS area: elements go in at their (row, column) from the MFMA
-// layout (lane l, register r hold row 8*(r/4) + 4*(l/32) + r%4, column
-// l%32 of a 32x32 block), then lanes read back whole 16-byte chunks of
-// strip rows and write them to global memory, 8..32 lanes per output row.
-// Strip rows are padded by 16 bytes so the two half-waves of a write land on
-// different banks.
-template <class OutT, int COLS>
+// Two phases per 32-row strip of a wave's sub-tile, through a private LDS
+// area (the idle operand ring):
+//   1. raw 32-bit accumulators go in at their (row, column) from the MFMA
+//      layout (lane l, register r hold row 8*(r/4) + 4*(l/32) + r%4, column
+//      l%32 of a 32x32 block) -- straight-line register moves only;
+//   2. a compact loop: each lane takes 4 consecutive columns of one row,
+//      applies the epilogue arithmetic once per element and stores the 4
+//      outputs as one 8- or 16-byte chunk (16 lanes cover 64 columns).
+// Pair strips hold gate and up accumulators side by side (2 words per
+// output). Strip rows are padded by 16 bytes so the two half-waves of a
+// phase-1 write land on different banks.
+template <int WORDS>          // 32-bit words per strip row
 struct Strip {
-  static constexpr int kRowB = COLS * (int)sizeof(OutT);
-  static constexpr int kStride = kRowB + 16;
+  static constexpr int kStride = WORDS * 4 + 16;
   static constexpr int kBytes = 32 * kStride;
-  static constexpr int kCPR = kRowB / 16;                 // 16-byte chunks per row
-  static constexpr int kPerLane = 32 * kCPR / 64;
-  static_assert(kPerLane >= 1 && kPerLane * 64 == 32 * kCPR, "strip must split over a wave");
 };
 
-template <class OutT, int COLS, class Epi>
-__device__ __forceinline__ void strip_flush(const uint8_t* lds, int64_t m0, int64_t n0, int64_t M,
-                                            int64_t N, const Epi& epi) {
-  using St = Strip<OutT, COLS>;
-  constexpr int EPC = 16 / (int)sizeof(OutT);             // elements per chunk
-  const int lane = threadIdx.x & 63;
-  __builtin_amdgcn_s_waitcnt(0xc07f);                     // lgkmcnt(0): strip writes landed
-  __builtin_amdgcn_wave_barrier();
-#pragma unroll
-  for (int k = 0; k < St::kPerLane; ++k) {
-    const int c = lane + 64 * k;
-    const int row = c / St::kCPR, ch = c % St::kCPR;
-    const int64_t m = m0 + row, n = n0 + ch * EPC;
-    const i32x4 v = *reinterpret_cast<const i32x4*>(lds + row * St::kStride + ch * 16);
-    if (m >= M || n >= N) continue;
-    if (epi.vec && n + EPC <= N) {
-      *reinterpret_cast<i32x4*>(epi.row(m) + n * (int64_t)sizeof(OutT)) = v;
-    } else {
-      const OutT* e = reinterpret_cast<const OutT*>(&v);
-      for (int q = 0; q < EPC && n + q < N; ++q) epi.put(m, n + q, e[q]);
-    }
-  }
-  __builtin_amdgcn_s_waitcnt(0xc07f);                     // reads done before the next strip
+__device__ __forceinline__ void lds_fence_wave() {
+  __builtin_amdgcn_s_waitcnt(0xc07f);                     // lgkmcnt(0)
   __builtin_amdgcn_wave_barrier();
 }
 
 template <int TM, int TN, class Acc, class Epi>
 __device__ __forceinline__ void epilogue_single(const Acc (&acc)[TM][TN], int64_t m0, int64_t n0,
                                                 int64_t M, int64_t N, const Epi& epi, uint8_t* lds) {
-  using OutT = typename Epi::OutT;
+  using Scalar = std::remove_cv_t<std::remove_reference_t<decltype(acc[0][0][0])>>;
   constexpr int COLS = TN * 32;
-  using St = Strip<OutT, COLS>;
+  using St = Strip<COLS>;
   const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
       const int col = j * 32 + (lane & 31);
-      const int64_t n = n0 + col;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int row = (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-        const int64_t m = m0 + i * 32 + row;
-        const OutT v = (m < M && n < N) ? epi.value(m, n, acc[i][j][r]) : OutT(0);
-        *reinterpret_cast<OutT*>(lds + row * St::kStride + col * (int)sizeof(OutT)) = v;
+        *reinterpret_cast<Scalar*>(lds + row * St::kStride + col * 4) = acc[i][j][r];
       }
     }
-    strip_flush<OutT, COLS>(lds, m0 + i * 32, n0, M, N, epi);
+    lds_fence_wave();
+    const int64_t mb = m0 + i * 32;
+    constexpr int G = COLS / 4;                           // 4-column groups per row
+#pragma unroll 2
+    for (int g = lane; g < 32 * G; g += 64) {
+      const int row = g / G, c4 = (g % G) * 4;
+      const int64_t m = mb + row, n = n0 + c4;
+      if (m >= M || n >= N) continue;
+      const Scalar* raw = reinterpret_cast<const Scalar*>(lds + row * St::kStride + c4 * 4);
+      const Scalar v[4] = {raw[0], raw[1], raw[2], raw[3]};
+      const int nv = N - n < 4 ? (int)(N - n) : 4;
+      store_group(epi, m, n, nv, epi.value4(m, n, v, nv));
+    }
+    lds_fence_wave();
   }
 }
 
 // Pair epilogue: blocks 2t (gate) and 2t+1 (up) give the same 32 output
-// columns c0 + 32 t + lane%32.
+// columns c0 + 32 t + lane%32; the strip interleaves them per column.
 template <int TM, int TN, class Acc, class Epi>
 __device__ __forceinline__ void epilogue_pair(const Acc (&acc)[TM][TN], int64_t m0, int64_t c0,
                                               int64_t M, int64_t NC, const Epi& epi, uint8_t* lds) {
-  using OutT = typename Epi::OutT;
   constexpr int COLS = TN / 2 * 32;
-  using St = Strip<OutT, COLS>;
+  using St = Strip<2 * COLS>;
   const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
 #pragma unroll
     for (int t = 0; t < TN / 2; ++t) {
       const int colw = t * 32 + (lane & 31);
-      const int64_t col = c0 + colw;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int row = (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-        const int64_t m = m0 + i * 32 + row;
-        const OutT v = (m < M && col < NC) ? epi.pair(m, col, acc[i][2 * t][r], acc[i][2 * t + 1][r]) : OutT(0);
-        *reinterpret_cast<OutT*>(lds + row * St::kStride + colw * (int)sizeof(OutT)) = v;
+        int32_t* p = reinterpret_cast<int32_t*>(lds + row * St::kStride + colw * 8);
+        p[0] = acc[i][2 * t][r];
+        p[1] = acc[i][2 * t + 1][r];
       }
     }
-    strip_flush<OutT, COLS>(lds, m0 + i * 32, c0, M, NC, epi);
+    lds_fence_wave();
+    const int64_t mb = m0 + i * 32;
+    constexpr int G = COLS / 4;
+#pragma unroll 2
+    for (int g = lane; g < 32 * G; g += 64) {
+      const int row = g / G, c4 = (g % G) * 4;
+      const int64_t m = mb + row, n = c0 + c4;
+      if (m >= M || n >= NC) continue;
+      const int32_t* raw = reinterpret_cast<const int32_t*>(lds + row * St::kStride + c4 * 8);
+      const int32_t gv[4] = {raw[0], raw[2], raw[4], raw[6]};
+      const int32_t uv[4] = {raw[1], raw[3], raw[5], raw[7]};
+      const int nv = NC - n < 4 ? (int)(NC - n) : 4;
+      store_group(epi, m, n, nv, epi.pair4(m, n, gv, uv, nv));
+    }
+    lds_fence_wave();
   }
 }
 
@@ -517,8 +520,7 @@ gemm_tile_kernel(GemmShape sh, Src2 sa, Src2 sb, const float* b_scale, Epi epi) 
   __syncthreads();
 
   // per-wave output strips in the (now idle) ring
-  using OutT = typename Epi::OutT;
-  constexpr int kStripBytes = Strip<OutT, (PAIR ? TN / 2 : TN) * 32>::kBytes;
+  constexpr int kStripBytes = Strip<(PAIR ? TN / 2 * 2 : TN) * 32>::kBytes;
   static_assert(kStripBytes * WM * WN <= NBUF * STAGE, "output strips exceed the LDS ring");
   uint8_t* strip = smem + wave * kStripBytes;
   const int64_t wm0 = m0 + wm * (TM * 32);

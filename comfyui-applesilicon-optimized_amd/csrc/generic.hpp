@@ -4,6 +4,7 @@
 // aligned rows, K a multiple of 16) and share the epilogue functors, so the
 // stored arithmetic is identical; only the speed differs.
 #pragma once
+#include "epilogues.hpp"
 #include "numerics.hpp"
 
 namespace c4q {
@@ -65,7 +66,8 @@ gemm_generic_kernel(int64_t M, int64_t N, int64_t K, int64_t nbx, Op op, Epi epi
   const Epi ep = epi.prepare();
   typename Op::Acc acc = 0;
   for (int64_t k = 0; k < K; ++k) acc = acc + op.av(m, k) * op.bv(n, k);
-  ep.put(m, n, ep.value(m, n, acc));
+  const typename Op::Acc v[4] = {acc, 0, 0, 0};
+  store_group(ep, m, n, 1, ep.value4(m, n, v, 1));
 }
 
 // FFN pair fallback: gate/up accumulators for output column `col`.
@@ -84,7 +86,8 @@ pair_generic_kernel(int64_t M, int64_t NC, int64_t K, int64_t nbx, const int8_t*
     ag += x * (int32_t)g[col * ldw + k];
     au += x * (int32_t)u[col * ldw + k];
   }
-  ep.put(m, col, ep.pair(m, col, ag, au));
+  const int32_t gv[4] = {ag, 0, 0, 0}, uv[4] = {au, 0, 0, 0};
+  store_group(ep, m, col, 1, ep.pair4(m, col, gv, uv, 1));
 }
 
 }  // namespace c4q
