@@ -416,6 +416,17 @@ __device__ __forceinline__ void wait_vm() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// Stage barrier without a memory fence. __syncthreads() is a workgroup
+// release/acquire fence, which makes the compiler wait for every
+// outstanding vector-memory operation (vmcnt(0)) -- that would drain the
+// whole copy ring at every stage. Here each wave has already waited for the
+// copies of the stage it needs (wait_vm); it waits for its own LDS reads,
+// then meets the others at the hardware barrier. The asm statement is also a
+// compiler barrier for memory operations.
+__device__ __forceinline__ void stage_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // PAIR = false: plain GEMM, epilogue(m, n, acc).
 // PAIR = true : gate/up pair, epilogue.pair(m, col, acc_gate, acc_up).
 // b_scale: W8A16 per-tensor weight scale (device pointer) or null.
@@ -472,7 +483,7 @@ gemm_tile_kernel(GemmShape sh, Src2 sa, Src2 sb, const float* b_scale, Epi epi) 
     lb.issue(rb0, rb1, buf + BM * SA, p * SB, b_kb);
   }
   wait_vm<(NBUF - 1) * kPerStage>();
-  __syncthreads();
+  stage_barrier();
 
   // K-step pipeline: the fragments of the next step are read while the
   // current step multiplies. The stage barrier sits before the last step of
@@ -494,7 +505,7 @@ gemm_tile_kernel(GemmShape sh, Src2 sa, Src2 sb, const float* b_scale, Epi epi) 
     for (int s = 0; s < S; ++s) {
       if (s == S - 1) {
         wait_vm<(NBUF - 2) * kPerStage>();     // this wave's copies of stage st+1 landed
-        __syncthreads();                       // ... and every wave's; stage st fully read
+        stage_barrier();                       // ... and every wave's; stage st fully read
         const int ps = st + NBUF;              // refill stage st's buffer (past K: zeros)
         uint8_t* buf = smem + (st % NBUF) * STAGE;
         la.issue(ra, ra, buf, ps * SA, a_kb);
