@@ -9,12 +9,20 @@
 // kernels):
 //   OutT                       stored element type (16- or 32-bit bits)
 //   prepare()                  per-workgroup copy with scalars loaded
-//   value4(m, n, v, nv)        packed outputs of elements (m, n .. n+3) from
-//                              accumulators v[0..3]; only the first nv are
-//                              valid (the rest are never read or stored)
-//   pair4(m, n, g, u, nv)      (pair epilogues) the same from gate/up sums
+//   Col, col(n, nv)            the parameters of columns n .. n+3 (scales,
+//                              bias); only the first nv are valid (the rest
+//                              repeat column n and are never stored)
+//   rowp(m)                    the parameter of row m (a scale, or 0)
+//   apply(r, c, v)             packed outputs of 4 elements of one row from
+//                              accumulators v[0..3] and the row / column
+//                              parameters; pair epilogues: apply(r, c, g, u)
+//                              from gate / up sums
+//   value4(m, n, v, nv)        = apply(rowp(m), col(n, nv), v)
 //   row(m), vec                byte pointer to output row m; rows are
 //                              16-byte aligned (chunked stores allowed)
+// The tiled kernels load a lane's column parameters once per tile and its
+// row parameters once per 32-row block, so the store loop does no loads
+// besides activation-table lookups.
 //
 // Neutral elements keep absent terms branch-free and exact: an absent scale
 // multiplies by 1.0f (x * 1 == x for every x), an absent bias adds -0.0f
@@ -77,9 +85,15 @@ __device__ __forceinline__ Packed pack_bf16x4(float a, float b, float c, float d
 // Raw INT32 store: torch._int_mm / i8_matmul2d_nt
 // (reference _patches/int8_ext/int8_gemm.mm:81-94).
 struct EpiI32 : EpiOut<uint32_t> {
+  struct Col {};
   __device__ __forceinline__ EpiI32 prepare() const { return *this; }
-  __device__ __forceinline__ uint4 value4(int64_t, int64_t, const int32_t (&v)[4], int) const {
+  __device__ __forceinline__ Col col(int64_t, int) const { return {}; }
+  __device__ __forceinline__ float rowp(int64_t) const { return 0.0f; }
+  __device__ __forceinline__ uint4 apply(float, const Col&, const int32_t (&v)[4]) const {
     return uint4{(uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]};
+  }
+  __device__ __forceinline__ uint4 value4(int64_t m, int64_t n, const int32_t (&v)[4], int nv) const {
+    return apply(rowp(m), col(n, nv), v);
   }
 };
 
@@ -88,18 +102,24 @@ struct EpiI32 : EpiOut<uint32_t> {
 // (reference _patches/int8_ext/int8_gemm.mm:97-122).
 struct EpiRowScale : EpiOut<uint16_t> {
   const float* rs; const uint16_t* bias;
+  struct Col { float b[4]; };
   __device__ __forceinline__ EpiRowScale prepare() const { return *this; }
-  __device__ __forceinline__ uint2 value4(int64_t m, int64_t n, const int32_t (&v)[4], int nv) const {
-    const float r = rs[m];
-    uint2 p = pack_bf16x4<uint2>((float)v[0] * r, (float)v[1] * r, (float)v[2] * r, (float)v[3] * r);
-    if (bias) {
-      float b[4];
+  __device__ __forceinline__ Col col(int64_t n, int nv) const {
+    Col c;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) b[q] = bf16_f32(bias[colq(n, q, nv)]);
-      p = pack_bf16x4<uint2>(bf16lo(p.x) + b[0], bf16hi(p.x) + b[1], bf16lo(p.y) + b[2],
-                             bf16hi(p.y) + b[3]);
-    }
+    for (int q = 0; q < 4; ++q) c.b[q] = bias ? bf16_f32(bias[colq(n, q, nv)]) : 0.0f;
+    return c;
+  }
+  __device__ __forceinline__ float rowp(int64_t m) const { return rs[m]; }
+  __device__ __forceinline__ uint2 apply(float r, const Col& c, const int32_t (&v)[4]) const {
+    uint2 p = pack_bf16x4<uint2>((float)v[0] * r, (float)v[1] * r, (float)v[2] * r, (float)v[3] * r);
+    if (bias)
+      p = pack_bf16x4<uint2>(bf16lo(p.x) + c.b[0], bf16hi(p.x) + c.b[1], bf16lo(p.y) + c.b[2],
+                             bf16hi(p.y) + c.b[3]);
     return p;
+  }
+  __device__ __forceinline__ uint2 value4(int64_t m, int64_t n, const int32_t (&v)[4], int nv) const {
+    return apply(rowp(m), col(n, nv), v);
   }
 };
 
@@ -108,21 +128,30 @@ struct EpiRowScale : EpiOut<uint16_t> {
 // (reference _patches/int8_ext/int8_gemm.mm:417-443).
 struct EpiRowColScale : EpiOut<uint16_t> {
   const float* rs; const float* cs; const uint16_t* bias;
+  struct Col { float s[4], b[4]; };
   __device__ __forceinline__ EpiRowColScale prepare() const { return *this; }
-  __device__ __forceinline__ uint2 value4(int64_t m, int64_t n, const int32_t (&v)[4], int nv) const {
-    const float r = rs[m];
+  __device__ __forceinline__ Col col(int64_t n, int nv) const {
+    Col c;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      c.s[q] = cs[colq(n, q, nv)];
+      c.b[q] = bias ? bf16_f32(bias[colq(n, q, nv)]) : 0.0f;
+    }
+    return c;
+  }
+  __device__ __forceinline__ float rowp(int64_t m) const { return rs[m]; }
+  __device__ __forceinline__ uint2 apply(float r, const Col& c, const int32_t (&v)[4]) const {
     float x[4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) x[q] = (float)v[q] * (cs[colq(n, q, nv)] * r);
+    for (int q = 0; q < 4; ++q) x[q] = (float)v[q] * (c.s[q] * r);
     uint2 p = pack_bf16x4<uint2>(x[0], x[1], x[2], x[3]);
-    if (bias) {
-      float b[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) b[q] = bf16_f32(bias[colq(n, q, nv)]);
-      p = pack_bf16x4<uint2>(bf16lo(p.x) + b[0], bf16hi(p.x) + b[1], bf16lo(p.y) + b[2],
-                             bf16hi(p.y) + b[3]);
-    }
+    if (bias)
+      p = pack_bf16x4<uint2>(bf16lo(p.x) + c.b[0], bf16hi(p.x) + c.b[1], bf16lo(p.y) + c.b[2],
+                             bf16hi(p.y) + c.b[3]);
     return p;
+  }
+  __device__ __forceinline__ uint2 value4(int64_t m, int64_t n, const int32_t (&v)[4], int nv) const {
+    return apply(rowp(m), col(n, nv), v);
   }
 };
 
@@ -150,14 +179,24 @@ struct EpiScaled : EpiOut<typename std::conditional<F32OUT, uint32_t, uint16_t>:
     e.sr0 = sr ? sr[0] : 1.0f;
     return e;
   }
-  __device__ __forceinline__ Packed value4(int64_t m, int64_t n, const float (&v)[4], int nv) const {
-    const float a = sa[m * sa_step];
+  struct Col { float s[4], b[4]; };
+  __device__ __forceinline__ Col col(int64_t n, int nv) const {
+    Col c;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      c.s[q] = sb[colq(n, q, nv) * sb_step];
+      c.b[q] = bias ? load_f32(bias, bias_dt, colq(n, q, nv)) : 0.0f;
+    }
+    return c;
+  }
+  __device__ __forceinline__ float rowp(int64_t m) const { return sa[m * sa_step]; }
+  __device__ __forceinline__ Packed apply(float a, const Col& c, const float (&v)[4]) const {
     float o[4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) o[q] = ((v[q] * a) * sb[colq(n, q, nv) * sb_step]) * sr0;
+    for (int q = 0; q < 4; ++q) o[q] = ((v[q] * a) * c.s[q]) * sr0;
     if (bias) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) o[q] = o[q] + load_f32(bias, bias_dt, colq(n, q, nv));
+      for (int q = 0; q < 4; ++q) o[q] = o[q] + c.b[q];
     }
     if constexpr (F32OUT) {
       return Packed{f32_bits(o[0]), f32_bits(o[1]), f32_bits(o[2]), f32_bits(o[3])};
@@ -165,6 +204,9 @@ struct EpiScaled : EpiOut<typename std::conditional<F32OUT, uint32_t, uint16_t>:
       if (out_dt == DT_F16) return Packed{f16x2_rne(o[0], o[1]), f16x2_rne(o[2], o[3])};
       return pack_bf16x4<Packed>(o[0], o[1], o[2], o[3]);
     }
+  }
+  __device__ __forceinline__ Packed value4(int64_t m, int64_t n, const float (&v)[4], int nv) const {
+    return apply(rowp(m), col(n, nv), v);
   }
 };
 
@@ -178,12 +220,20 @@ struct EpiW8A16 : EpiOut<typename std::conditional<F32OUT, uint32_t, uint16_t>::
   using Base = EpiOut<typename std::conditional<F32OUT, uint32_t, uint16_t>::type>;
   using Packed = typename Base::Packed;
   int out_dt; const void* bias; int bias_dt; const uint16_t* act;
+  struct Col { float b[4]; };
   __device__ __forceinline__ EpiW8A16 prepare() const { return *this; }
-  __device__ __forceinline__ Packed value4(int64_t, int64_t n, const float (&v)[4], int nv) const {
+  __device__ __forceinline__ Col col(int64_t n, int nv) const {
+    Col c;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) c.b[q] = bias ? load_f32(bias, bias_dt, colq(n, q, nv)) : 0.0f;
+    return c;
+  }
+  __device__ __forceinline__ float rowp(int64_t) const { return 0.0f; }
+  __device__ __forceinline__ Packed apply(float, const Col& c, const float (&v)[4]) const {
     float o[4] = {v[0], v[1], v[2], v[3]};
     if (bias) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) o[q] = o[q] + load_f32(bias, bias_dt, colq(n, q, nv));
+      for (int q = 0; q < 4; ++q) o[q] = o[q] + c.b[q];
     }
     if constexpr (F32OUT) {
       return Packed{f32_bits(o[0]), f32_bits(o[1]), f32_bits(o[2]), f32_bits(o[3])};
@@ -197,6 +247,9 @@ struct EpiW8A16 : EpiOut<typename std::conditional<F32OUT, uint32_t, uint16_t>::
       return p;
     }
   }
+  __device__ __forceinline__ Packed value4(int64_t m, int64_t n, const float (&v)[4], int nv) const {
+    return apply(rowp(m), col(n, nv), v);
+  }
 };
 
 // Fused gate/up FFN pair. Both projections use the per-channel epilogue
@@ -209,16 +262,25 @@ struct EpiW8A16 : EpiOut<typename std::conditional<F32OUT, uint32_t, uint16_t>::
 struct EpiPair : EpiOut<uint16_t> {
   const float* rs; const float* s1; const float* s2;
   const uint16_t* t1; const uint16_t* t2;
+  struct Col { float s1[4], s2[4]; };
   __device__ __forceinline__ EpiPair prepare() const { return *this; }
-  __device__ __forceinline__ uint2 pair4(int64_t m, int64_t n, const int32_t (&g)[4],
-                                         const int32_t (&u)[4], int nv) const {
-    const float r = rs[m];
+  __device__ __forceinline__ Col col(int64_t n, int nv) const {
+    Col c;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      c.s1[q] = s1[colq(n, q, nv)];
+      c.s2[q] = s2[colq(n, q, nv)];
+    }
+    return c;
+  }
+  __device__ __forceinline__ float rowp(int64_t m) const { return rs[m]; }
+  __device__ __forceinline__ uint2 apply(float r, const Col& c, const int32_t (&g)[4],
+                                         const int32_t (&u)[4]) const {
     float a[4], b[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int64_t c = colq(n, q, nv);
-      a[q] = (float)g[q] * (s1[c] * r);
-      b[q] = (float)u[q] * (s2[c] * r);
+      a[q] = (float)g[q] * (c.s1[q] * r);
+      b[q] = (float)u[q] * (c.s2[q] * r);
     }
     uint2 x1 = pack_bf16x4<uint2>(a[0], a[1], a[2], a[3]);
     uint2 x2 = pack_bf16x4<uint2>(b[0], b[1], b[2], b[3]);
@@ -233,6 +295,10 @@ struct EpiPair : EpiOut<uint16_t> {
     return pack_bf16x4<uint2>(bf16lo(x1.x) * bf16lo(x2.x), bf16hi(x1.x) * bf16hi(x2.x),
                               bf16lo(x1.y) * bf16lo(x2.y), bf16hi(x1.y) * bf16hi(x2.y));
   }
+  __device__ __forceinline__ uint2 pair4(int64_t m, int64_t n, const int32_t (&g)[4],
+                                         const int32_t (&u)[4], int nv) const {
+    return apply(rowp(m), col(n, nv), g, u);
+  }
 };
 
 // Store a packed group of 4 outputs at (m, n .. n+nv-1).
@@ -244,8 +310,11 @@ __device__ __forceinline__ void store_group(const Epi& epi, int64_t m, int64_t n
     *reinterpret_cast<Packed*>(dst) = p;
     return;
   }
-  const OutT* e = reinterpret_cast<const OutT*>(&p);
-  for (int q = 0; q < nv; ++q) reinterpret_cast<OutT*>(dst)[q] = e[q];
+  OutT e[4];
+  __builtin_memcpy(e, &p, sizeof(e));
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    if (q < nv) reinterpret_cast<OutT*>(dst)[q] = e[q];
 }
 
 }  // namespace c4q

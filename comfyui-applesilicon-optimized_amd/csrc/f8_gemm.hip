@@ -44,11 +44,11 @@ extern "C" int c4q_f8_gemm_nt_scaled(const uint8_t* a, int64_t lda, const uint8_
   if (d_dtype == C4Q_F32) {
     EpiScaled<true> epi{{d, ldd, rows_vec16(d, ldd, 4)}, d_dtype, scale_a, scale_a_mode, scale_b,
                         scale_b_mode, scale_result, bias, bias_dtype, 0, 0, 1.0f};
-    return run_gemm8<OpF8, GenF8>(a, lda, b, ldb, M, N, K, epi, as_stream(stream), what);
+    return run_gemm8<OpF8Any, GenF8>(a, lda, b, ldb, M, N, K, epi, as_stream(stream), what);
   }
   EpiScaled<false> epi{{d, ldd, rows_vec16(d, ldd, 2)}, d_dtype, scale_a, scale_a_mode, scale_b,
                        scale_b_mode, scale_result, bias, bias_dtype, 0, 0, 1.0f};
-  return run_gemm8<OpF8, GenF8>(a, lda, b, ldb, M, N, K, epi, as_stream(stream), what);
+  return run_gemm8<OpF8Any, GenF8>(a, lda, b, ldb, M, N, K, epi, as_stream(stream), what);
 }
 
 namespace {

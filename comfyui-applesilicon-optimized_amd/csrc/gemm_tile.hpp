@@ -9,21 +9,25 @@
 // Structure:
 //   * a workgroup of WM x WN wave64s owns a BM x BN output tile; each wave a
 //     (BM/WM) x (BN/WN) sub-tile of 32x32 MFMA blocks held in registers;
-//   * K advances in stages of 64 elements. Operands are copied global ->
+//   * K advances in stages of 64 or 128 elements (a policy constant). Operands are copied global ->
 //     LDS by buffer_load_dwordx4 ... lds (no register round trip) into a
 //     ring of NBUF stage buffers, issued up to NBUF-1 stages ahead of the
 //     MFMAs that consume them, so the copy latency (~1.3 us from L2/MALL)
 //     hides behind several stages of MFMA work; one barrier per stage;
 //   * inside a stage the LDS fragments of the next K step are read while the
 //     current step multiplies, across stage boundaries too;
-//   * the epilogue stages each wave's accumulators through LDS, then applies
-//     the output arithmetic in a compact loop over 4-column groups and
-//     stores whole 8/16-byte chunks of output rows;
+//   * the kernel is persistent: each workgroup walks a sequence of tiles
+//     with one copy ring, so the next tile's first stages are copied while
+//     the current tile's epilogue runs;
+//   * the epilogue stages each wave's accumulators through a small private
+//     LDS strip, applies the output arithmetic with column / row parameters
+//     loaded once per tile and stores whole 8/16-byte chunks of output rows;
 //   * the copy reads through buffer resources based at the tile origin whose
 //     range ends at the matrix end: tail rows and the K tail read as zero in
 //     hardware (stages past K are issued with out-of-range offsets, so every
 //     stage issues the same number of copies);
-//   * LDS rows are 64 or 128 bytes per stage with the 16-byte chunks
+//   * LDS rows are 64 or 128 bytes per stage (8-bit operands at 128 K per
+//     stage move whole 128-byte cache lines) with the 16-byte chunks
 //     XOR-swizzled by row, so that fragment reads (32 lanes on 32 rows, one
 //     chunk) are bank-conflict free;
 //   * W8A16: the fp8 weight is staged as fp8 and dequantized to bf16/f16 in
@@ -34,6 +38,7 @@
 //     B panels a band shares inside that XCD's L2.
 #pragma once
 #include <type_traits>
+#include <utility>
 
 #include "epilogues.hpp"
 #include "numerics.hpp"
@@ -50,7 +55,6 @@ typedef __bf16   bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8  __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2  __attribute__((ext_vector_type(2)));
 
-constexpr int kStageK = 64;          // K elements per pipeline stage
 constexpr int kGroupM = 8;           // tile rows per raster band
 
 template <class T, class F>
@@ -98,18 +102,28 @@ struct DirectLoad {
   static constexpr int kWaves = NT / 64;
   static constexpr int kInstr = ROWS / RPI / kWaves;
   static_assert(kInstr >= 1 && kInstr * RPI * kWaves == ROWS, "tile rows must split over the waves");
-  int voff[kInstr];
-  int kofs[kInstr];           // byte offset of this lane's chunk within the stage row
+  // The swizzles repeat every 16 rows and one copy round of all waves spans
+  // a multiple of 16 rows, so a lane's chunk within the stage row is the
+  // same for every copy it issues.
+  static_assert((RPI * kWaves) % 16 == 0, "swizzle period must divide the copy round");
+  // Source offsets: plain operands step by a fixed number of rows per copy
+  // (one base register and a uniform stride); pair operands interleave the
+  // gate and up matrices by 32-row block and keep one offset per copy.
+  static constexpr int kOff = PAIR ? kInstr : 1;
+  int voff[kOff];
+  int kofs;                   // byte offset of this lane's chunk within the stage row
+  int step;                   // plain operands: bytes between the rows of consecutive copies
   __device__ __forceinline__ void init(int64_t ld_bytes) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    kofs = ((lane % CPR) ^ Swz<ROWB>::f(RPI * wave + lane / CPR)) * 16;
+    step = (int)(RPI * kWaves * ld_bytes);
 #pragma unroll
-    for (int j = 0; j < kInstr; ++j) {
+    for (int j = 0; j < kOff; ++j) {
       const int q = wave + kWaves * j;
       const int r = RPI * q + lane / CPR;                      // LDS row
       const int blk = (RPI * q) >> 5;
       const int src = PAIR ? ((blk >> 1) * 32 + ((RPI * q) & 31) + lane / CPR) : r;
-      kofs[j] = ((lane % CPR) ^ Swz<ROWB>::f(r)) * 16;
-      voff[j] = (int)(src * ld_bytes) + kofs[j];
+      voff[j] = (int)(src * ld_bytes) + kofs;
     }
   }
   // Copy K bytes [kb, kb + ROWB) of every row into `lds`; bytes at or past
@@ -117,13 +131,15 @@ struct DirectLoad {
   __device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t r0, __amdgpu_buffer_rsrc_t r1,
                                         uint8_t* lds, int kb, int k_bytes) const {
     const int wave = threadIdx.x >> 6;
+    const bool in_k = kb + kofs < k_bytes;
 #pragma unroll
     for (int j = 0; j < kInstr; ++j) {
       const int q = wave + kWaves * j;
       const __amdgpu_buffer_rsrc_t rs = (PAIR && (((RPI * q) >> 5) & 1)) ? r1 : r0;
-      const int vo = kb + kofs[j] < k_bytes ? voff[j] : kOOB;
+      const int vo = PAIR ? voff[PAIR ? j : 0] : voff[0] + j * step;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rs, (__attribute__((address_space(3))) void*)(lds + (RPI * q) * ROWB), 16, vo, kb, 0, 0);
+          rs, (__attribute__((address_space(3))) void*)(lds + (RPI * q) * ROWB), 16,
+          in_k ? vo : kOOB, kb, 0, 0);
     }
   }
 };
@@ -163,10 +179,11 @@ __device__ __forceinline__ i32x4 lds_chunk(const uint8_t* sm, int r, int c) {
 // kernel reads step s+1 while step s multiplies.
 
 // int8 x int8 -> int32, v_mfma_i32_32x32x32_i8: a lane holds 16 K values
-// (one chunk); a 64-byte stage row is 2 K steps.
-struct OpI8 {
+// (one chunk); a stage of KS K values (KS-byte rows) is KS/32 K steps.
+template <int KS>
+struct OpI8T {
   using Acc = i32x16;
-  static constexpr int SA = 64, SB = 64, S = 2;
+  static constexpr int kStageK = KS, SA = KS, SB = KS, S = KS / 32;
   template <int TM, int TN> struct Frag { i32x4 a[TM], b[TN]; };
   __device__ __forceinline__ static float prep_scale(const float*) { return 1.0f; }
   template <int TM, int TN>
@@ -190,28 +207,27 @@ struct OpI8 {
 
 // OCP e4m3 x e4m3 -> fp32, v_mfma_f32_32x32x64_f8f6f4 (cbsz = blgp = 0:
 // e4m3 operands; zero scales: unscaled): a lane holds 32 K values (two
-// chunks); a 64-byte stage row is one K step.
-struct OpF8 {
+// chunks); a stage of KS K values is KS/64 K steps.
+template <int KS>
+struct OpF8T {
   using Acc = f32x16;
-  static constexpr int SA = 64, SB = 64, S = 1;
+  static constexpr int kStageK = KS, SA = KS, SB = KS, S = KS / 64;
   template <int TM, int TN> struct Frag { i32x8 a[TM], b[TN]; };
   __device__ __forceinline__ static float prep_scale(const float*) { return 1.0f; }
+  template <int ROWB>
+  __device__ __forceinline__ static i32x8 pair_chunks(const uint8_t* sm, int r, int c) {
+    const i32x4 x = lds_chunk<ROWB>(sm, r, c);
+    const i32x4 y = lds_chunk<ROWB>(sm, r, c + 1);
+    return i32x8{x.x, x.y, x.z, x.w, y.x, y.y, y.z, y.w};
+  }
   template <int TM, int TN>
   __device__ __forceinline__ static void frags(Frag<TM, TN>& f, const uint8_t* sa, const uint8_t* sb,
-                                               int ra0, int rb0, int) {
+                                               int ra0, int rb0, int s) {
     const int lane = threadIdx.x & 63, lr = lane & 31, h = lane >> 5;
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      const i32x4 x = lds_chunk<SA>(sa, ra0 + i * 32 + lr, 2 * h);
-      const i32x4 y = lds_chunk<SA>(sa, ra0 + i * 32 + lr, 2 * h + 1);
-      f.a[i] = i32x8{x.x, x.y, x.z, x.w, y.x, y.y, y.z, y.w};
-    }
+    for (int i = 0; i < TM; ++i) f.a[i] = pair_chunks<SA>(sa, ra0 + i * 32 + lr, 4 * s + 2 * h);
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const i32x4 x = lds_chunk<SB>(sb, rb0 + j * 32 + lr, 2 * h);
-      const i32x4 y = lds_chunk<SB>(sb, rb0 + j * 32 + lr, 2 * h + 1);
-      f.b[j] = i32x8{x.x, x.y, x.z, x.w, y.x, y.y, y.z, y.w};
-    }
+    for (int j = 0; j < TN; ++j) f.b[j] = pair_chunks<SB>(sb, rb0 + j * 32 + lr, 4 * s + 2 * h);
   }
   template <int TM, int TN>
   __device__ __forceinline__ static void mma(const Frag<TM, TN>& f, Acc (&acc)[TM][TN], float) {
@@ -223,6 +239,10 @@ struct OpF8 {
                                                                     0, 0, 0, 0);
   }
 };
+// The fp8 policy always stages 128 K (two K steps; the pipeline needs an
+// even step count), whatever stage depth a tile asks of 8-bit policies.
+template <int KS>
+using OpF8Any = OpF8T<128>;
 
 // W8A16: bf16 (or f16) activations x fp8 weights dequantized in registers,
 // v_mfma_f32_32x32x16_{bf16,f16}: a lane holds 8 K values. A stage row is
@@ -236,7 +256,7 @@ struct OpF8 {
 template <bool BF16, bool HAS_SCALE>
 struct OpW8A16 {
   using Acc = f32x16;
-  static constexpr int SA = 128, SB = 64, S = 2;
+  static constexpr int kStageK = 64, SA = 128, SB = 64, S = 2;
   template <int TM, int TN> struct Frag { i32x4 a[2][TM], q[TN]; };
   // per-tensor weight scale rounded to the activation type (scale.to(T))
   __device__ __forceinline__ static float prep_scale(const float* sp) {
@@ -300,21 +320,30 @@ __device__ __forceinline__ TileCoord tile_of(int bid, int nblocks, int tiles_m, 
 }
 
 // ------------------------------------------------------------ epilogue ---
-// Two phases per 32-row strip of a wave's sub-tile, through a private LDS
-// area (the idle operand ring):
+// Per 8-row group of each 32-row MFMA block of a wave's sub-tile, through a
+// private 8-row LDS strip that lies outside the operand ring (the ring holds
+// the next tile's first stages by then):
 //   1. raw 32-bit accumulators go in at their (row, column) from the MFMA
 //      layout (lane l, register r hold row 8*(r/4) + 4*(l/32) + r%4, column
-//      l%32 of a 32x32 block) -- straight-line register moves only;
-//   2. a compact loop: each lane takes 4 consecutive columns of one row,
-//      applies the epilogue arithmetic once per element and stores the 4
-//      outputs as one 8- or 16-byte chunk (16 lanes cover 64 columns).
-// Pair strips hold gate and up accumulators side by side (2 words per
-// output). Strip rows are padded by 16 bytes so the two half-waves of a
-// phase-1 write land on different banks.
+//      l%32 of a 32x32 block; group q is registers 4q .. 4q+3) -- register
+//      moves only;
+//   2. each lane takes one row (lane/8) and applies the epilogue to store
+//      units of UNIT consecutive columns (16 bytes of output, at most the
+//      lane's share): unit h of lane l starts at column UNIT*(8h + l%8), so
+//      one store instruction writes 8 whole 16-byte chunks per row, one
+//      128-byte line.
+// A lane's columns are the same for the whole tile, so their parameters
+// (scales, bias) are loaded once per tile; its row parameters are loaded once
+// per tile as well (TM*4 rows). Pair strips hold gate and up accumulators
+// side by side (2 words per output column).
 template <int WORDS>          // 32-bit words per strip row
 struct Strip {
-  static constexpr int kStride = WORDS * 4 + 16;
-  static constexpr int kBytes = 32 * kStride;
+  static_assert(WORDS >= 64, "strip rows must span both bank halves");
+  static constexpr int kBytes = 8 * WORDS * 4;
+  // Rows 4..7 (written by the upper half-wave) keep their words XOR-ed by
+  // 32, so the two halves of a phase-1 write land on different banks; runs
+  // of 4 aligned words stay contiguous.
+  __device__ __forceinline__ static int word(int r, int w) { return r * WORDS + (w ^ ((r & 4) << 3)); }
 };
 
 __device__ __forceinline__ void lds_fence_wave() {
@@ -322,38 +351,112 @@ __device__ __forceinline__ void lds_fence_wave() {
   __builtin_amdgcn_wave_barrier();
 }
 
+// Lane layout of the store phase for COLS output columns of OutT.
+template <int COLS, class OutT>
+struct StoreMap {
+  static constexpr int CPL = COLS / 8;                                  // columns per lane
+  static constexpr int UNIT = (16 / (int)sizeof(OutT)) < CPL ? 16 / (int)sizeof(OutT) : CPL;
+  static constexpr int UPL = CPL / UNIT;                                // units per lane
+  static constexpr int GPU = UNIT / 4;                                  // 4-column groups per unit
+  static constexpr int NG = CPL / 4;                                    // groups per lane
+  static_assert(UNIT % 4 == 0 && UPL * UNIT == CPL, "bad store map");
+  // first column (relative to the sub-tile) of group g = h * GPU + gg
+  __device__ __forceinline__ static int col(int lane, int g) {
+    return UNIT * ((g / GPU) * 8 + (lane & 7)) + 4 * (g % GPU);
+  }
+};
+
+// Store one unit (GPU packed 4-column groups) at (m, n .. n+nv-1): one 8- or
+// 16-byte store where the row allows, else per group.
+template <int GPU, class Epi, class Packed>
+__device__ __forceinline__ void store_unit(const Epi& epi, int64_t m, int64_t n, int nv,
+                                           const Packed* p) {
+  using OutT = typename Epi::OutT;
+  if (epi.vec && nv >= 4 * GPU) {
+    uint8_t* dst = epi.row(m) + n * (int64_t)sizeof(OutT);
+    if constexpr (sizeof(Packed) == 8 && GPU == 2)
+      *reinterpret_cast<uint4*>(dst) = uint4{p[0].x, p[0].y, p[1].x, p[1].y};
+    else
+      *reinterpret_cast<Packed*>(dst) = p[0];
+    return;
+  }
+#pragma unroll
+  for (int gg = 0; gg < GPU; ++gg) {
+    const int k = nv - 4 * gg;
+    if (k > 0) store_group(epi, m, n + 4 * gg, k < 4 ? k : 4, p[gg]);
+  }
+}
+
+// Column parameters of a lane's groups; groups at or past N load nothing
+// (nothing is stored for them).
+template <class Map, class Epi>
+__device__ __forceinline__ void load_cols(const Epi& epi, int64_t n0, int64_t N, int lane,
+                                          typename Epi::Col (&col)[Map::NG]) {
+#pragma unroll
+  for (int g = 0; g < Map::NG; ++g) {
+    const int64_t c = n0 + Map::col(lane, g);
+    const int64_t k = N - c;
+    col[g] = typename Epi::Col{};
+    if (k > 0) col[g] = epi.col(c, k < 4 ? (int)k : 4);
+  }
+}
+
+template <int TM, class Epi>
+__device__ __forceinline__ void load_rows(const Epi& epi, int64_t m0, int64_t M, int prow,
+                                          float (&rp)[TM][4]) {
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int64_t m = m0 + i * 32 + q * 8 + prow;
+      rp[i][q] = 0.0f;                       // rows past M load nothing
+      if (m < M) rp[i][q] = epi.rowp(m);
+    }
+}
+
 template <int TM, int TN, class Acc, class Epi>
 __device__ __forceinline__ void epilogue_single(const Acc (&acc)[TM][TN], int64_t m0, int64_t n0,
                                                 int64_t M, int64_t N, const Epi& epi, uint8_t* lds) {
   using Scalar = std::remove_cv_t<std::remove_reference_t<decltype(acc[0][0][0])>>;
   constexpr int COLS = TN * 32;
+  using Map = StoreMap<COLS, typename Epi::OutT>;
   using St = Strip<COLS>;
-  const int lane = threadIdx.x & 63;
+  using Packed = typename Epi::Packed;
+  Scalar* sw = reinterpret_cast<Scalar*>(lds);
+  const int lane = threadIdx.x & 63, prow = lane >> 3;
+  typename Epi::Col col[Map::NG];
+  load_cols<Map>(epi, n0, N, lane, col);
+  float rp[TM][4];
+  load_rows<TM>(epi, m0, M, prow, rp);
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int col = j * 32 + (lane & 31);
+    for (int q = 0; q < 4; ++q) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-        *reinterpret_cast<Scalar*>(lds + row * St::kStride + col * 4) = acc[i][j][r];
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          sw[St::word((lane >> 5) * 4 + r, j * 32 + (lane & 31))] = acc[i][j][4 * q + r];
+      lds_fence_wave();
+      const int64_t m = m0 + i * 32 + q * 8 + prow;
+      if (m < M) {
+#pragma unroll
+        for (int h = 0; h < Map::UPL; ++h) {
+          const int c = Map::col(lane, h * Map::GPU);
+          const int64_t nv = N - (n0 + c);
+          if (nv <= 0) continue;
+          Packed out[Map::GPU];
+#pragma unroll
+          for (int gg = 0; gg < Map::GPU; ++gg) {
+            const Scalar* w = sw + St::word(prow, c + 4 * gg);
+            const Scalar v[4] = {w[0], w[1], w[2], w[3]};
+            out[gg] = epi.apply(rp[i][q], col[h * Map::GPU + gg], v);
+          }
+          store_unit<Map::GPU>(epi, m, n0 + c, nv < Map::UNIT ? (int)nv : Map::UNIT, out);
+        }
       }
+      lds_fence_wave();
     }
-    lds_fence_wave();
-    const int64_t mb = m0 + i * 32;
-    constexpr int G = COLS / 4;                           // 4-column groups per row
-#pragma unroll 2
-    for (int g = lane; g < 32 * G; g += 64) {
-      const int row = g / G, c4 = (g % G) * 4;
-      const int64_t m = mb + row, n = n0 + c4;
-      if (m >= M || n >= N) continue;
-      const Scalar* raw = reinterpret_cast<const Scalar*>(lds + row * St::kStride + c4 * 4);
-      const Scalar v[4] = {raw[0], raw[1], raw[2], raw[3]};
-      const int nv = N - n < 4 ? (int)(N - n) : 4;
-      store_group(epi, m, n, nv, epi.value4(m, n, v, nv));
-    }
-    lds_fence_wave();
   }
 }
 
@@ -363,36 +466,47 @@ template <int TM, int TN, class Acc, class Epi>
 __device__ __forceinline__ void epilogue_pair(const Acc (&acc)[TM][TN], int64_t m0, int64_t c0,
                                               int64_t M, int64_t NC, const Epi& epi, uint8_t* lds) {
   constexpr int COLS = TN / 2 * 32;
+  using Map = StoreMap<COLS, typename Epi::OutT>;
   using St = Strip<2 * COLS>;
-  const int lane = threadIdx.x & 63;
+  int32_t* sw = reinterpret_cast<int32_t*>(lds);
+  const int lane = threadIdx.x & 63, prow = lane >> 3;
+  typename Epi::Col col[Map::NG];
+  load_cols<Map>(epi, c0, NC, lane, col);
+  float rp[TM][4];
+  load_rows<TM>(epi, m0, M, prow, rp);
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
 #pragma unroll
-    for (int t = 0; t < TN / 2; ++t) {
-      const int colw = t * 32 + (lane & 31);
+    for (int q = 0; q < 4; ++q) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-        int32_t* p = reinterpret_cast<int32_t*>(lds + row * St::kStride + colw * 8);
-        p[0] = acc[i][2 * t][r];
-        p[1] = acc[i][2 * t + 1][r];
+      for (int t = 0; t < TN / 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int x = St::word((lane >> 5) * 4 + r, 2 * (t * 32 + (lane & 31)));
+          sw[x] = acc[i][2 * t][4 * q + r];
+          sw[x + 1] = acc[i][2 * t + 1][4 * q + r];
+        }
+      lds_fence_wave();
+      const int64_t m = m0 + i * 32 + q * 8 + prow;
+      if (m < M) {
+#pragma unroll
+        for (int h = 0; h < Map::UPL; ++h) {
+          const int c = Map::col(lane, h * Map::GPU);
+          const int64_t nv = NC - (c0 + c);
+          if (nv <= 0) continue;
+          uint2 out[Map::GPU];
+#pragma unroll
+          for (int gg = 0; gg < Map::GPU; ++gg) {
+            const int32_t* w = sw + St::word(prow, 2 * (c + 4 * gg));
+            const int32_t gv[4] = {w[0], w[2], w[4], w[6]};
+            const int32_t uv[4] = {w[1], w[3], w[5], w[7]};
+            out[gg] = epi.apply(rp[i][q], col[h * Map::GPU + gg], gv, uv);
+          }
+          store_unit<Map::GPU>(epi, m, c0 + c, nv < Map::UNIT ? (int)nv : Map::UNIT, out);
+        }
       }
+      lds_fence_wave();
     }
-    lds_fence_wave();
-    const int64_t mb = m0 + i * 32;
-    constexpr int G = COLS / 4;
-#pragma unroll 2
-    for (int g = lane; g < 32 * G; g += 64) {
-      const int row = g / G, c4 = (g % G) * 4;
-      const int64_t m = mb + row, n = c0 + c4;
-      if (m >= M || n >= NC) continue;
-      const int32_t* raw = reinterpret_cast<const int32_t*>(lds + row * St::kStride + c4 * 8);
-      const int32_t gv[4] = {raw[0], raw[2], raw[4], raw[6]};
-      const int32_t uv[4] = {raw[1], raw[3], raw[5], raw[7]};
-      const int nv = NC - n < 4 ? (int)(NC - n) : 4;
-      store_group(epi, m, n, nv, epi.pair4(m, n, gv, uv, nv));
-    }
-    lds_fence_wave();
   }
 }
 
@@ -403,7 +517,7 @@ struct GemmShape {
 };
 
 // Operand sources: base pointers and strides; each workgroup derives its
-// tile's buffer resources from them.
+// tiles' buffer resources from them.
 struct Src2 {
   const uint8_t* p0; const uint8_t* p1;   // p1: second matrix of a pair (up rows), else = p0
   int64_t ld_bytes; int64_t rows;          // rows of each matrix
@@ -427,6 +541,15 @@ __device__ __forceinline__ void stage_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// Bytes of one wave's epilogue strip.
+template <int TN, bool PAIR>
+constexpr int strip_bytes() { return Strip<(PAIR ? TN / 2 * 2 : TN) * 32>::kBytes; }
+
+// Persistent kernel: workgroup b takes tiles b, b + G, b + 2G, ... (G =
+// gridDim.x) in the XCD-aware order of tile_of, and runs one copy ring
+// through all of them: the last stages of a tile already copy the next
+// tile's first stages, which land while the epilogue stores.
+//
 // PAIR = false: plain GEMM, epilogue(m, n, acc).
 // PAIR = true : gate/up pair, epilogue.pair(m, col, acc_gate, acc_up).
 // b_scale: W8A16 per-tensor weight scale (device pointer) or null.
@@ -437,51 +560,67 @@ gemm_tile_kernel(GemmShape sh, Src2 sa, Src2 sb, const float* b_scale, Epi epi) 
   constexpr int TM = BM / WM / 32, TN = BN / WN / 32;   // 32x32 MFMA blocks per wave
   static_assert(TM >= 1 && TN >= 1 && TM * WM * 32 == BM && TN * WN * 32 == BN, "bad wave tiling");
   static_assert(!PAIR || (TN % 2 == 0), "pair tiles need whole gate/up block pairs");
-  constexpr int SA = Op::SA, SB = Op::SB;
+  constexpr int SA = Op::SA, SB = Op::SB, S = Op::S;
+  static_assert(S % 2 == 0, "the fragment double buffer assumes an even step count per stage");
   constexpr int STAGE = BM * SA + BN * SB;
-  static_assert(NBUF >= 2 && NBUF * STAGE <= 160 * 1024, "LDS ring exceeds 160 KB");
+  constexpr int RING = NBUF * STAGE;
+  constexpr int kStrip = strip_bytes<TN, PAIR>();
+  static_assert(NBUF >= 2 && RING + kStrip * WM * WN <= 160 * 1024, "LDS exceeds 160 KB");
   using LA = DirectLoad<BM, SA, NT, false>;
   using LB = DirectLoad<BN, SB, NT, PAIR>;
   constexpr int kPerStage = LA::kInstr + LB::kInstr;     // copies per wave per stage
   static_assert((NBUF - 1) * kPerStage < 64, "too many copies in flight for vmcnt");
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[NBUF * STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[RING + kStrip * WM * WN];
 
-  const TileCoord tc = tile_of(blockIdx.x, gridDim.x, sh.tiles_m, sh.tiles_n);
+  const int ntiles = sh.tiles_m * sh.tiles_n;
+  const int G = (int)gridDim.x;
+  const int my_tiles = (ntiles - 1 - (int)blockIdx.x) / G + 1;
   const Epi ep = epi.prepare();
-  const int64_t m0 = (int64_t)tc.tm * BM;
-  const int64_t n0 = (int64_t)tc.tn * BN;
   const int wave = threadIdx.x >> 6;
   const int wm = wave / WN, wn = wave % WN;
+  const float ws = Op::prep_scale(b_scale);
 
   LA la;
   LB lb;
   la.init(sa.ld_bytes);
   lb.init(sb.ld_bytes);
-  const __amdgpu_buffer_rsrc_t ra = make_rsrc(sa.p0 + m0 * sa.ld_bytes, (sa.rows - m0) * sa.ld_bytes);
-  const int64_t brow0 = PAIR ? (n0 >> 1) : n0;     // pair: both matrices start at column n0/2
-  const int64_t bleft = (sb.rows - brow0) * sb.ld_bytes;
-  const __amdgpu_buffer_rsrc_t rb0 = make_rsrc(sb.p0 + brow0 * sb.ld_bytes, bleft);
-  const __amdgpu_buffer_rsrc_t rb1 = PAIR ? make_rsrc(sb.p1 + brow0 * sb.ld_bytes, bleft) : rb0;
-  const float ws = Op::prep_scale(b_scale);
+  constexpr int KS = Op::kStageK;
+  const int a_kb = (int)(sh.K * SA / KS), b_kb = (int)(sh.K * SB / KS);
+  const int nst = (int)((sh.K + KS - 1) / KS);
 
-  typename Op::Acc acc[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
-
-  const int a_kb = (int)(sh.K * (SA / kStageK)), b_kb = (int)(sh.K * (SB / kStageK));
-  const int nst = (int)((sh.K + kStageK - 1) / kStageK);
+  // Copy cursor: next stage to issue is stage ips of this workgroup's tile ij.
+  int ij = 0, ips = 0;
+  __amdgpu_buffer_rsrc_t ra, rb0, rb1;
+  auto tile_rsrc = [&](int j) {
+    const TileCoord tc = tile_of((int)blockIdx.x + j * G, ntiles, sh.tiles_m, sh.tiles_n);
+    const int64_t m0 = (int64_t)tc.tm * BM;
+    const int64_t brow0 = PAIR ? ((int64_t)tc.tn * BN >> 1) : (int64_t)tc.tn * BN;
+    const int64_t bleft = (sb.rows - brow0) * sb.ld_bytes;
+    ra = make_rsrc(sa.p0 + m0 * sa.ld_bytes, (sa.rows - m0) * sa.ld_bytes);
+    rb0 = make_rsrc(sb.p0 + brow0 * sb.ld_bytes, bleft);
+    rb1 = PAIR ? make_rsrc(sb.p1 + brow0 * sb.ld_bytes, bleft) : rb0;
+  };
+  // Issue the next stage into `buf`; past this workgroup's last tile the
+  // copies read zeros (every stage issues the same number of copies, which
+  // keeps the vmcnt arithmetic fixed).
+  auto issue_next = [&](uint8_t* buf) {
+    if (ij < my_tiles) {
+      la.issue(ra, ra, buf, ips * SA, a_kb);
+      lb.issue(rb0, rb1, buf + BM * SA, ips * SB, b_kb);
+      if (++ips == nst) {
+        ips = 0;
+        if (++ij < my_tiles) tile_rsrc(ij);
+      }
+    } else {
+      la.issue(ra, ra, buf, 0, 0);
+      lb.issue(rb0, rb1, buf + BM * SA, 0, 0);
+    }
+  };
+  tile_rsrc(0);
 
   // prologue: stages 0 .. NBUF-1 in flight, stage 0 complete and visible
 #pragma unroll
-  for (int p = 0; p < NBUF; ++p) {
-    uint8_t* buf = smem + p * STAGE;
-    la.issue(ra, ra, buf, p * SA, a_kb);
-    lb.issue(rb0, rb1, buf + BM * SA, p * SB, b_kb);
-  }
+  for (int p = 0; p < NBUF; ++p) issue_next(smem + p * STAGE);
   wait_vm<(NBUF - 1) * kPerStage>();
   stage_barrier();
 
@@ -493,54 +632,46 @@ gemm_tile_kernel(GemmShape sh, Src2 sa, Src2 sb, const float* b_scale, Epi epi) 
   const int ra0 = wm * (TM * 32), rb0i = wn * (TN * 32);
   using Frag = typename Op::template Frag<TM, TN>;
   Frag fr[2];
-  Op::template frags<TM, TN>(fr[0], smem, smem + BM * SA, ra0, rb0i, 0);
-  constexpr int S = Op::S;
-  // One stage; P = parity of the stage's first K step in the global step
-  // sequence (so the fragment double buffer is indexed statically).
-  auto run_stage = [&](int st, auto Pc) {
-    constexpr int P = decltype(Pc)::value;
-    const uint8_t* cur = smem + (st % NBUF) * STAGE;
-    const uint8_t* nxt = smem + ((st + 1) % NBUF) * STAGE;
+  uint8_t* strip = smem + RING + wave * kStrip;
+  int gs = 0;                                   // stage counter over all tiles
+  for (int j = 0; j < my_tiles; ++j) {
+    typename Op::Acc acc[TM][TN];
 #pragma unroll
-    for (int s = 0; s < S; ++s) {
-      if (s == S - 1) {
-        wait_vm<(NBUF - 2) * kPerStage>();     // this wave's copies of stage st+1 landed
-        stage_barrier();                       // ... and every wave's; stage st fully read
-        const int ps = st + NBUF;              // refill stage st's buffer (past K: zeros)
-        uint8_t* buf = smem + (st % NBUF) * STAGE;
-        la.issue(ra, ra, buf, ps * SA, a_kb);
-        lb.issue(rb0, rb1, buf + BM * SA, ps * SB, b_kb);
-        Op::template frags<TM, TN>(fr[(P + s + 1) & 1], nxt, nxt + BM * SA, ra0, rb0i, 0);
-      } else {
-        Op::template frags<TM, TN>(fr[(P + s + 1) & 1], cur, cur + BM * SA, ra0, rb0i, s + 1);
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int jj = 0; jj < TN; ++jj)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][jj][r] = 0;
+    {
+      const uint8_t* cur = smem + (gs % NBUF) * STAGE;
+      Op::template frags<TM, TN>(fr[0], cur, cur + BM * SA, ra0, rb0i, 0);
+    }
+    for (int st = 0; st < nst; ++st, ++gs) {
+      uint8_t* cur = smem + (gs % NBUF) * STAGE;
+      const uint8_t* nxt = smem + ((gs + 1) % NBUF) * STAGE;
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        if (s == S - 1) {
+          wait_vm<(NBUF - 2) * kPerStage>();   // this wave's copies of stage gs+1 landed
+          stage_barrier();                     // ... and every wave's; stage gs fully read
+          issue_next(cur);                     // refill with stage gs+NBUF
+          if (st + 1 < nst) Op::template frags<TM, TN>(fr[0], nxt, nxt + BM * SA, ra0, rb0i, 0);
+        } else {
+          Op::template frags<TM, TN>(fr[(s + 1) & 1], cur, cur + BM * SA, ra0, rb0i, s + 1);
+        }
+        Op::template mma<TM, TN>(fr[s & 1], acc, ws);
       }
-      Op::template mma<TM, TN>(fr[(P + s) & 1], acc, ws);
     }
-  };
-  if constexpr (S % 2 == 0) {
-    for (int st = 0; st < nst; ++st) run_stage(st, std::integral_constant<int, 0>{});
-  } else {
-    int st = 0;
-    for (; st + 1 < nst; st += 2) {
-      run_stage(st, std::integral_constant<int, 0>{});
-      run_stage(st + 1, std::integral_constant<int, 1>{});
+    const TileCoord tc = tile_of((int)blockIdx.x + j * G, ntiles, sh.tiles_m, sh.tiles_n);
+    const int64_t wm0 = (int64_t)tc.tm * BM + wm * (TM * 32);
+    if constexpr (PAIR) {
+      const int64_t c0 = ((int64_t)tc.tn * BN >> 1) + wn * (TN * 16);
+      epilogue_pair<TM, TN>(acc, wm0, c0, sh.M, sh.N >> 1, ep, strip);
+    } else {
+      epilogue_single<TM, TN>(acc, wm0, (int64_t)tc.tn * BN + wn * (TN * 32), sh.M, sh.N, ep, strip);
     }
-    if (st < nst) run_stage(st, std::integral_constant<int, 0>{});
   }
-  wait_vm<0>();    // past-K copies still land in the ring; drain before reusing LDS
-  __syncthreads();
-
-  // per-wave output strips in the (now idle) ring
-  constexpr int kStripBytes = Strip<(PAIR ? TN / 2 * 2 : TN) * 32>::kBytes;
-  static_assert(kStripBytes * WM * WN <= NBUF * STAGE, "output strips exceed the LDS ring");
-  uint8_t* strip = smem + wave * kStripBytes;
-  const int64_t wm0 = m0 + wm * (TM * 32);
-  if constexpr (PAIR) {
-    const int64_t c0 = (n0 >> 1) + wn * (TN * 16);
-    epilogue_pair<TM, TN>(acc, wm0, c0, sh.M, sh.N >> 1, ep, strip);
-  } else {
-    epilogue_single<TM, TN>(acc, wm0, n0 + wn * (TN * 32), sh.M, sh.N, ep, strip);
-  }
+  wait_vm<0>();    // zero-fill copies past the last tile still target the ring
 }
 
 }  // namespace c4q

@@ -29,7 +29,7 @@ extern "C" int c4q_i8_gemm_nt_i32(const int8_t* a, int64_t lda, const int8_t* b,
   int st = check_i8_args(a, lda, b, ldb, c, ldc, M, N, K, what);
   if (st) return st;
   EpiI32 epi{{c, ldc, rows_vec16(c, ldc, 4)}};
-  return run_gemm8<OpI8, GenI8>(reinterpret_cast<const uint8_t*>(a), lda,
+  return run_gemm8<OpI8T, GenI8>(reinterpret_cast<const uint8_t*>(a), lda,
                                  reinterpret_cast<const uint8_t*>(b), ldb, M, N, K, epi,
                                  as_stream(stream), what);
 }
@@ -43,7 +43,7 @@ extern "C" int c4q_i8_gemm_nt_fused(const int8_t* a, int64_t lda, const int8_t* 
   if (st) return st;
   C4Q_REQUIRE(M == 0 || N == 0 || row_scale != nullptr, C4Q_ERR_ARG, "%s: null row_scale", what);
   EpiRowScale epi{{d, ldd, rows_vec16(d, ldd, 2)}, row_scale, bias};
-  return run_gemm8<OpI8, GenI8>(reinterpret_cast<const uint8_t*>(a), lda,
+  return run_gemm8<OpI8T, GenI8>(reinterpret_cast<const uint8_t*>(a), lda,
                                  reinterpret_cast<const uint8_t*>(b), ldb, M, N, K, epi,
                                  as_stream(stream), what);
 }
@@ -58,7 +58,7 @@ extern "C" int c4q_i8_gemm_nt_fused_cs(const int8_t* a, int64_t lda, const int8_
   C4Q_REQUIRE(M == 0 || N == 0 || (row_scale != nullptr && col_scale != nullptr), C4Q_ERR_ARG,
               "%s: null row_scale/col_scale", what);
   EpiRowColScale epi{{d, ldd, rows_vec16(d, ldd, 2)}, row_scale, col_scale, bias};
-  return run_gemm8<OpI8, GenI8>(reinterpret_cast<const uint8_t*>(a), lda,
+  return run_gemm8<OpI8T, GenI8>(reinterpret_cast<const uint8_t*>(a), lda,
                                  reinterpret_cast<const uint8_t*>(b), ldb, M, N, K, epi,
                                  as_stream(stream), what);
 }
@@ -93,6 +93,6 @@ extern "C" int c4q_i8_ffn_pair(const int8_t* a, int64_t lda, const int8_t* w_gat
                 ldw, N_out};
   return with_tile(pick_tile(M, 2 * N_out), [&](auto t) {
     using T = decltype(t);
-    return launch_tile<T, OpI8, true>(sh, 2 * N_out, sa, sb, nullptr, epi, s, what);
+    return launch_tile<T, OpI8T<T::KS8>, true>(sh, 2 * N_out, sa, sb, nullptr, epi, s, what);
   });
 }

@@ -315,7 +315,7 @@ def test_moss_pair_exact(dev):
 
 # ---------------------------------------------------- every tile variant ---
 
-@pytest.mark.parametrize("tile", ["0", "1", "2", "3"])
+@pytest.mark.parametrize("tile", [str(t) for t in range(7)])
 def test_every_tile_variant(dev, monkeypatch, tile):
     """Force each MFMA tile variant (C4Q_TILE) on ragged shapes: INT8 fused
     epilogue and pair bit-exact, fp8 / W8A16 within tolerance."""
