@@ -1,6 +1,7 @@
 // FP8 e4m3fn x e4m3fn scaled GEMM (torch._scaled_mm semantics) and the
 // W8A16 (bf16/f16 activation x fp8 weight) linear.
 #include "launch.hpp"
+#include "skinny.hpp"
 
 using namespace c4q;
 
@@ -52,11 +53,55 @@ extern "C" int c4q_f8_gemm_nt_scaled(const uint8_t* a, int64_t lda, const uint8_
 }
 
 namespace {
+// Small-M route: 16-row weight blocks, K split over the waves of a
+// persistent workgroup (4 chunks of 64 per wave, up to 16 waves), the blocks
+// dealt to as many workgroups as fit on the device in one round (balanced
+// rounds).
+template <bool BF16, bool HAS_SCALE, class Epi>
+int run_w8a16_skinny(const uint16_t* a, int64_t lda, const uint8_t* w, int64_t ldw,
+                     const float* w_scale, int64_t M, int64_t N, int64_t K, const Epi& epi,
+                     hipStream_t s, const char* what) {
+  const int64_t nblk = cdiv(N, 16);
+  const int64_t nch = cdiv(K, 64);
+  auto launch = [&](auto kernel, int cpw, int maxw, int& occ) {
+    const int waves = (int)cdiv(nch, cpw);
+    if (occ <= 0) {
+      int o = 0;
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, kernel, 64 * maxw, 0) != hipSuccess || o < 1)
+        o = 1;
+      occ = o;
+    }
+    // occupancy was taken at the largest block size; smaller blocks fit at
+    // least as many workgroups per CU
+    const int64_t slots = (int64_t)device_cus() * occ * (maxw / waves);
+    const int64_t rounds = cdiv(nblk, slots);
+    const int64_t grid = cdiv(nblk, rounds);
+    hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(64 * waves), 0, s, a, lda, w, ldw, w_scale,
+                       M, N, K, epi);
+    return check_launch(what);
+  };
+  static int occ4 = 0;
+  return launch(w8a16_skinny_kernel<BF16, HAS_SCALE, 4, kSkinnyMaxWaves, Epi>, 4, kSkinnyMaxWaves, occ4);
+}
+
 template <class Epi>
 int run_w8a16(const void* a, int a_dtype, int64_t lda, const uint8_t* w, int64_t ldw,
               const float* w_scale, int64_t M, int64_t N, int64_t K, const Epi& epi, hipStream_t s,
               const char* what) {
   const bool bf16 = a_dtype == C4Q_BF16;
+  // The skinny kernel addresses a 16-row weight block and the activation
+  // rows with 32-bit buffer offsets.
+  const bool skinny = M <= kSkinnyMaxM && K > 0 && K <= kSkinnyMaxK && aligned16(a) &&
+                      aligned16(w) && lda % 8 == 0 && ldw % 16 == 0 && 16 * ldw + 64 < (1ll << 31) &&
+                      kSkinnyMaxM * 2 * lda + 256 < (1ll << 31);
+  if (skinny) {
+    const uint16_t* a16 = static_cast<const uint16_t*>(a);
+    if (bf16)
+      return w_scale ? run_w8a16_skinny<true, true>(a16, lda, w, ldw, w_scale, M, N, K, epi, s, what)
+                     : run_w8a16_skinny<true, false>(a16, lda, w, ldw, w_scale, M, N, K, epi, s, what);
+    return w_scale ? run_w8a16_skinny<false, true>(a16, lda, w, ldw, w_scale, M, N, K, epi, s, what)
+                   : run_w8a16_skinny<false, false>(a16, lda, w, ldw, w_scale, M, N, K, epi, s, what);
+  }
   const bool tiled = K > 0 && K % 16 == 0 && aligned16(a) && aligned16(w) && lda % 8 == 0 &&
                      ldw % 16 == 0 && tile_offsets_fit(2 * lda, ldw);
   if (!tiled) {

@@ -53,15 +53,34 @@ int with_tile(int id, F&& f) {
   }
 }
 
-// Tile choice: the largest tile that still gives every CU work. A tile id in
-// the environment variable C4Q_TILE (0..6) overrides it, for tuning sweeps.
+// Tile choice by a cost model of the persistent kernel: a tile variant runs
+// in ceil(tiles / slots) rounds (slots = CUs x resident workgroups per CU),
+// each costing one tile's MACs times the slots it fills, at the variant's
+// measured relative per-CU throughput on large shapes (MI355X, 8-bit
+// operands: 256x256 w8 1.00, 256x256 w4 0.90, 128x128 0.87, 64x128 0.70).
+// A tile id in the environment variable C4Q_TILE (0..6) overrides it, for
+// tuning sweeps.
 inline int pick_tile(int64_t M, int64_t N) {
   const char* env = getenv("C4Q_TILE");
   if (env && env[0] >= '0' && env[0] < '0' + TILE_COUNT && env[1] == 0) return env[0] - '0';
-  const int64_t cus = 256;
-  if (cdiv(M, 256) * cdiv(N, 256) >= 2 * cus) return TILE_256x256_W8;
-  if (cdiv(M, 128) * cdiv(N, 128) >= cus) return TILE_128x128_W4;
-  return TILE_64x128_W4;
+  struct Cand { int id, bm, bn, per_cu; double eff; };
+  static const Cand cands[] = {{TILE_256x256_W8, 256, 256, 1, 1.00},
+                               {TILE_128x128_W4_K128, 128, 128, 2, 0.87},
+                               {TILE_64x128_W4_K128, 64, 128, 2, 0.70}};
+  const double cus = 256;
+  int best = TILE_256x256_W8;
+  double best_cost = 0;
+  for (const Cand& c : cands) {
+    const double tiles = (double)(cdiv(M, c.bm) * cdiv(N, c.bn));
+    const double slots = cus * c.per_cu;
+    const double rounds = (double)(int64_t)((tiles + slots - 1) / slots);
+    const double cost = rounds * slots * c.bm * c.bn / c.eff;
+    if (c.id == TILE_256x256_W8 || cost < best_cost) {
+      best = c.id;
+      best_cost = cost;
+    }
+  }
+  return best;
 }
 
 // Compute units of the current device (cached per device id).

@@ -262,6 +262,56 @@ def test_w8a16_linear(dev, M, K, N, xdt, scaled, bias_dt):
     assert_close(tof(bits16(out)), tof(ref), f"w8a16 {M}x{K}x{N}")
 
 
+@pytest.mark.parametrize("M,K,N,xdt,scaled,bias_dt,out_dt", [
+    (1, 3072, 3072, torch.bfloat16, True, torch.bfloat16, None),     # decode shapes (16 waves)
+    (4, 3072, 8200, torch.bfloat16, True, torch.bfloat16, None),     # 8-wave split, ragged N
+    (16, 3072, 3072, torch.bfloat16, False, None, None),
+    (16, 1040, 17, torch.bfloat16, True, torch.float32, None),       # K tail inside a chunk
+    (3, 24, 40, torch.bfloat16, True, torch.bfloat16, None),         # K < one chunk
+    (7, 4160, 300, torch.float16, True, torch.float32, None),        # f16 activations
+    (5, 3072, 260, torch.bfloat16, True, torch.bfloat16, torch.float32),
+    (17, 3072, 512, torch.bfloat16, True, torch.bfloat16, None),     # first M past the small-M route
+    (2, 4096, 96, torch.bfloat16, True, torch.bfloat16, None),       # largest K of the small-M route
+    (2, 4112, 96, torch.bfloat16, True, torch.bfloat16, None),       # K past it: tiled route
+    (16, 3072, 18432, torch.bfloat16, True, torch.bfloat16, None),   # several blocks per workgroup
+])
+def test_w8a16_small_m(dev, M, K, N, xdt, scaled, bias_dt, out_dt):
+    """Small-M (split-K) route against the oracle's dequant + fp32-accumulated
+    linear, within the bf16 output tolerance."""
+    g = gen(7 + M + K + N)
+    x = torch.randn(M, K, generator=g).to(xdt)
+    wf = 0.02 * torch.randn(N, K, generator=g)
+    ws = wf.abs().amax() / 448 if scaled else None
+    w = _fp8(wf / ws) if scaled else _fp8(wf * 20)
+    bias = (0.01 * torch.randn(N, generator=g)).to(bias_dt) if bias_dt is not None else None
+    out = ops.w8a16_linear(x.to(dev), w.to(dev), ws.reshape(1).to(dev) if scaled else None,
+                           bias.to(dev) if bias is not None else None, out_dtype=out_dt)
+    xd = "bf16" if xdt == torch.bfloat16 else "f16"
+    bd = {torch.bfloat16: "bf16", torch.float32: "f32", None: "f32"}[bias_dt]
+    braw = None if bias is None else (bits16(bias) if bias_dt == torch.bfloat16 else bias.numpy())
+    od = "f32" if out_dt == torch.float32 else xd
+    ref = of.w8a16_linear(bits16(x), u8(w), ws.numpy() if scaled else None, braw, bd, xd, od)
+    if od == "f32":
+        assert_close(out.cpu().numpy(), ref, f"w8a16 small-M f32 {M}x{K}x{N}")
+    else:
+        tof = bf16_bits_to_f32 if xd == "bf16" else f16_bits_to_f32
+        assert_close(tof(bits16(out)), tof(ref), f"w8a16 small-M {M}x{K}x{N}")
+
+
+def test_w8a16_small_m_gelu_table(dev):
+    """Activation table on the small-M route: exact lookup of its own bf16 linear output."""
+    g = gen(11)
+    M, K, N = 4, 3072, 1000
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    wf = 0.02 * torch.randn(N, K, generator=g)
+    ws = (wf.abs().amax() / 448).reshape(1)
+    w = _fp8(wf / ws)
+    table = torch.from_numpy(oact.gelu_tanh_table().view(np.int16))
+    lin = ops.w8a16_linear(x.to(dev), w.to(dev), ws.to(dev))
+    act = ops.w8a16_linear(x.to(dev), w.to(dev), ws.to(dev), act_table=table.to(dev))
+    assert_bits_equal(bits16(act), oact.apply_table(oact.gelu_tanh_table(), bits16(lin)), "gelu small-M")
+
+
 def test_w8a16_gelu_table_exact_on_bf16_result(dev):
     """GELU-tanh epilogue = table lookup of the rounded bf16 linear output."""
     g = gen(5)
