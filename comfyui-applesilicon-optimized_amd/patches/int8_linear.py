@@ -1,0 +1,205 @@
+"""comfy_kitchen ``int8_linear`` (W8A8) on ROCm through the int8 MFMA kernels.
+
+Mirrors ``_patches/int8_linear_kernel_mps.py`` (and the int8-fast seam of
+``_patches/int8_linear_mps.py``):
+
+* ``_int8_linear_kernel`` is the drop-in for comfy_kitchen's eager
+  ``int8_linear(x, weight, weight_scale, bias=None, out_dtype=bf16,
+  convrot=False, convrot_groupsize=256)`` (``:218-263``): per-row int8
+  activation quant, int8 x int8 -> int32 GEMM against the stored [N, K]
+  weight, rescale by ``weight_scale * x_scale``, optional bias;
+* ``_int8_linear_prequant`` dispatches by scale layout (``:152-215``): a
+  per-tensor scale with bf16 output uses the fused per-row epilogue
+  (``row_scale = weight_scale * x_scale``), a per-channel scale the fused
+  per-channel epilogue, anything else the raw int32 GEMM followed by the
+  reference's eager rescale (chunked ``C.float() * (w_scale * x_scale)``,
+  ``.to(out_dtype)``, ``+ bias``) on the GPU;
+* ``_quant_cached`` keeps a 1-slot cache of the quantized activation keyed
+  by a weak reference to the input tensor (``:97-140``), so the q/k/v (and
+  gate/up) projections of a block quantize their shared input once;
+* ``_try_int8_kernel_forward`` is the Linear.forward eligibility gate
+  (``:779-830``) and ``install`` wraps comfy's ``mixed_precision_ops``
+  factory (``:862-894``) when ComfyUI is importable;
+* ``int8_forward_dynamic[_per_row]`` replace int8-fast's wide-batch forwards
+  (``int8_linear_mps.py:54-63``) with the same W8A8 computation (the
+  reference re-routes them to a bf16 dequant + F.linear on MPS; on MI355X
+  the int8 kernel is the fast path).
+
+Not supported here (those calls keep the original function): ConvRot
+activation rotation (``convrot=True``; comfy_kitchen's Hadamard rounding is
+not pinned), non-int8 weights, tensors off the ROCm device.
+"""
+import os
+import weakref
+
+import torch
+
+from .. import ops
+from .._lib import C4QError
+from . import _common
+
+TAG = "[cdna4q/int8_linear]"
+
+_installed = False
+_orig_int8_linear = None
+_act_cache = None      # (x_weakref, convrot, groupsize, x_8, x_scale)
+_RESCALE_CHUNK_BYTES = 256 * 1024 * 1024
+
+
+def _quant_cached(x, convrot=False, convrot_groupsize=256):
+    """Rowwise-quantize x (reference ``:97-140``), reusing the previous result
+    when the same live tensor object is quantized again with the same
+    settings. Disable with ``C4Q_INT8_ACT_CACHE=0``."""
+    global _act_cache
+    if convrot:
+        raise C4QError(f"{TAG} ConvRot activation rotation is not supported by this build")
+    c = _act_cache
+    if c is not None and c[0]() is x and c[1] == convrot and c[2] == convrot_groupsize:
+        return c[3], c[4]
+    x_8, x_scale = ops.i8_quant_rowwise(x.reshape(-1, x.shape[-1]))
+    if os.environ.get("C4Q_INT8_ACT_CACHE", "1") != "0":
+        try:
+            _act_cache = (weakref.ref(x), convrot, convrot_groupsize, x_8, x_scale)
+        except TypeError:      # tensor subclass without weakref support
+            _act_cache = None
+    return x_8, x_scale
+
+
+def _int8_linear_prequant(x_8, x_scale, weight, weight_scale, bias, out_dtype, input_shape,
+                          split_tail=False):
+    """INT8 GEMM + epilogue from an already quantized activation (reference
+    ``:152-215``; ``split_tail`` only changes the reference's schedule and is
+    accepted for signature parity)."""
+    weight_scale = weight_scale.reshape(-1)
+    n = weight.shape[0]
+    out_shape = (*input_shape[:-1], n)
+    if out_dtype == torch.bfloat16 and weight_scale.numel() == 1:
+        row_scale = (weight_scale.float() * x_scale.reshape(-1).float()).contiguous()
+        bias_arg = bias.to(torch.bfloat16) if bias is not None else None
+        return ops.i8_matmul2d_nt_fused(x_8, weight, row_scale, bias_arg).reshape(out_shape)
+    if out_dtype == torch.bfloat16 and weight_scale.numel() == n:
+        bias_arg = bias.to(torch.bfloat16) if bias is not None else None
+        return ops.i8_matmul2d_nt_fused_cs(
+            x_8, weight, x_scale.reshape(-1).float().contiguous(),
+            weight_scale.float().contiguous(), bias_arg, split_tail).reshape(out_shape)
+    # eager rescale of the raw int32 product, as comfy_kitchen does it
+    result = ops.i8_matmul2d_nt(x_8, weight)
+    m = result.shape[0]
+    chunk = max(1, min(m, _RESCALE_CHUNK_BYTES // (n * 4)))
+    xs = x_scale.reshape(-1, 1)
+    parts = []
+    for i in range(0, m, chunk):
+        e = min(i + chunk, m)
+        parts.append((result[i:e].float() * (weight_scale * xs[i:e])).to(out_dtype))
+    result = torch.cat(parts, dim=0)
+    if bias is not None:
+        result = result + bias.to(device=result.device, dtype=result.dtype)
+    return result.reshape(out_shape)
+
+
+def _int8_linear_kernel(x, weight, weight_scale, bias=None, out_dtype=torch.bfloat16,
+                        convrot=False, convrot_groupsize=256):
+    """Kernel-backed drop-in for comfy_kitchen's eager ``int8_linear``
+    (reference ``:218-263``). Calls it cannot serve go to the original
+    function when one is installed, else raise."""
+    if (convrot or weight.dtype != torch.int8 or not _common.on_device(x, weight)
+            or x.dtype not in (torch.bfloat16, torch.float16)):
+        if _orig_int8_linear is not None:
+            return _orig_int8_linear(x, weight, weight_scale, bias, out_dtype, convrot,
+                                     convrot_groupsize)
+        raise C4QError(f"{TAG} call not supported (convrot={convrot}, weight {weight.dtype}, "
+                       f"x {x.dtype} on {x.device})")
+    x_8, x_scale = _quant_cached(x, convrot, convrot_groupsize)
+    return _int8_linear_prequant(x_8, x_scale, weight, weight_scale, bias, out_dtype, x.shape)
+
+
+int8_linear = _int8_linear_kernel
+
+
+def _try_int8_kernel_forward(self, input):
+    """Layer output via the kernel W8A8 path, or None to use comfy's forward
+    (reference ``:779-830``). Eligible iff the input is a plain tensor on the
+    ROCm device, the weight a TensorWiseINT8Layout QuantizedTensor without
+    ConvRot or transposition, and the layer has no full-precision flag,
+    force-cast or LoRA weight/bias functions."""
+    if not _common.on_device(input) or _common.is_quantized_int8(input):
+        return None
+    w = getattr(self, "weight", None)
+    if not _common.is_quantized_int8(w):
+        return None
+    if getattr(self, "_full_precision_mm", False) or getattr(self, "comfy_force_cast_weights", False):
+        return None
+    if len(getattr(self, "weight_function", [])) or len(getattr(self, "bias_function", [])):
+        return None
+    params = w._params
+    if getattr(params, "transposed", False) or getattr(params, "convrot", False):
+        return None
+    if input.dtype not in (torch.bfloat16, torch.float16):
+        return None
+    return _int8_linear_kernel(input, w._qdata, params.scale, self.bias, input.dtype)
+
+
+# ---------------------------------------------------------- int8-fast seam ---
+
+def _w8a8_dynamic(x, weight, weight_scale, bias, compute_dtype):
+    x_8, x_scale = _quant_cached(x)
+    return _int8_linear_prequant(x_8, x_scale, weight, weight_scale, bias, compute_dtype, x.shape)
+
+
+def int8_forward_dynamic(x, weight, weight_scale, bias, compute_dtype):
+    """int8-fast's per-tensor W8A8 forward (``x_8, x_s = quant(x)``;
+    ``_int_mm(x_8, w.T).float() * (w_scale * x_s)``; ``+ bias``), reference
+    seam ``int8_linear_mps.py:54-57``."""
+    return _w8a8_dynamic(x, weight, weight_scale, bias, compute_dtype)
+
+
+def int8_forward_dynamic_per_row(x, weight, weight_scale, bias, compute_dtype):
+    """int8-fast's per-output-channel W8A8 forward (reference seam
+    ``int8_linear_mps.py:60-63``)."""
+    return _w8a8_dynamic(x, weight, weight_scale, bias, compute_dtype)
+
+
+def install():
+    """Wrap comfy's ``mixed_precision_ops`` factory so generated int8 Linear
+    layers route through the kernel (reference ``:837-894``). Returns True
+    when installed (ComfyUI importable and a ROCm device present)."""
+    global _installed, _orig_int8_linear
+    if _installed:
+        return True
+    if not _common.rocm_available():
+        return False
+    try:
+        import comfy.ops as comfy_ops
+    except Exception:
+        return False
+    try:
+        from comfy_kitchen.backends.eager.quantization import int8_linear as orig
+        _orig_int8_linear = orig
+    except Exception:
+        _orig_int8_linear = None
+    factory = comfy_ops.mixed_precision_ops
+    if getattr(factory, "_c4q_wrapped", False):
+        _installed = True
+        return True
+
+    def wrapped_factory(*a, **k):
+        cls = factory(*a, **k)
+        linear_cls = getattr(cls, "Linear", None)
+        if linear_cls is not None and not getattr(linear_cls, "_c4q_int8_patched", False):
+            orig_forward = linear_cls.forward
+
+            def forward(self, input, *args, **kwargs):
+                res = _try_int8_kernel_forward(self, input)
+                if res is not None:
+                    return res
+                return orig_forward(self, input, *args, **kwargs)
+
+            linear_cls.forward = forward
+            linear_cls._c4q_int8_patched = True
+        return cls
+
+    wrapped_factory._c4q_wrapped = True
+    comfy_ops.mixed_precision_ops = wrapped_factory
+    _installed = True
+    print(f"{TAG} comfy int8 Linear layers routed to the int8 MFMA kernels.")
+    return True

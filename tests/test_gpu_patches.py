@@ -1,0 +1,151 @@
+"""The patch layer's seams on the GPU against the oracle: exact for the INT8
+routes (kitchen int8_linear, int8-fast, torch._int_mm, the FFN pairs), within
+the stated bf16 tolerance for the fp8 routes (torch._scaled_mm, the W8A16
+Linear forward)."""
+import types
+
+import numpy as np
+import pytest
+import torch
+
+from _util import assert_bits_equal, assert_close, bf16_to_f32, bits16, gen, u8
+from oracle import act as oact
+from oracle import fp8 as of
+from oracle import int8 as oi
+from oracle import pair as op
+
+import cdna4q.ops as ops
+from cdna4q.patches import int8_linear, int_mm, krea2_ffn_pair, linear_fp8_w8a16, moss_ffn, scaled_mm_fp8
+
+pytestmark = pytest.mark.gpu
+
+
+def _i8(shape, g):
+    return torch.randint(-127, 128, shape, generator=g, dtype=torch.int8)
+
+
+def test_patched_int_mm_exact(dev):
+    g = gen(21)
+    a, w = _i8((77, 640), g), _i8((300, 640), g)
+    assert int_mm.install()
+    try:
+        out = torch._int_mm(a.to(dev), w.to(dev).t())     # b = weight.T, the common caller form
+        ref = torch._int_mm(a, w.t())                      # CPU stock op (int64-exact)
+        assert torch.equal(out.cpu(), ref)
+        f = torch._int_mm(torch.ones(32, 32, device=dev, dtype=torch.int8),
+                          torch.ones(32, 32, device=dev, dtype=torch.int8))
+        assert int(f[0, 0]) == 32
+    finally:
+        int_mm.uninstall()
+
+
+@pytest.mark.parametrize("scale", ["tensor", "channel"])
+@pytest.mark.parametrize("bias", [False, True])
+def test_kitchen_int8_linear_exact(dev, scale, bias):
+    g = gen(22)
+    x = torch.randn(2, 150, 512, generator=g).to(torch.bfloat16)
+    w = _i8((384, 512), g)
+    ws = (torch.rand(1, generator=g) * 0.01) if scale == "tensor" else torch.rand(384, generator=g) * 0.01
+    b = torch.randn(384, generator=g).to(torch.bfloat16) if bias else None
+    int8_linear._act_cache = None
+    out = int8_linear.int8_linear(x.to(dev), w.to(dev), ws.to(dev), b.to(dev) if bias else None)
+    assert out.shape == (2, 150, 384)
+    ref = oi.int8_linear(bits16(x.reshape(-1, 512)), w.numpy(), ws.numpy(),
+                         bits16(b) if bias else None)
+    assert_bits_equal(bits16(out.reshape(-1, 384)), ref, f"int8_linear {scale} bias={bias}")
+
+
+def test_kitchen_int8_linear_f16_out_eager_rescale(dev):
+    """Non-bf16 output: raw int32 GEMM + comfy_kitchen's eager rescale,
+    identical to the same torch ops on the CPU."""
+    g = gen(23)
+    x = torch.randn(64, 256, generator=g).to(torch.bfloat16)
+    w = _i8((96, 256), g)
+    ws = torch.rand(96, generator=g) * 0.01
+    b = torch.randn(96, generator=g).to(torch.float16)
+    int8_linear._act_cache = None
+    out = int8_linear.int8_linear(x.to(dev), w.to(dev), ws.to(dev), b.to(dev), torch.float16)
+    q, xs = oi.quant_rowwise(bits16(x))
+    c = torch.from_numpy(oi.i8_matmul2d_nt(q, w.numpy()))
+    ref = (c.float() * (ws * torch.from_numpy(xs).reshape(-1, 1))).to(torch.float16) + b
+    assert torch.equal(out.cpu(), ref)
+
+
+def test_int8_fast_seam_exact(dev):
+    g = gen(24)
+    x = torch.randn(40, 512, generator=g).to(torch.bfloat16)
+    w = _i8((256, 512), g)
+    ws = torch.rand(1, generator=g) * 0.01
+    int8_linear._act_cache = None
+    out = int8_linear.int8_forward_dynamic(x.to(dev), w.to(dev), ws.to(dev), None, torch.bfloat16)
+    assert_bits_equal(bits16(out), oi.int8_linear(bits16(x), w.numpy(), ws.numpy()), "int8-fast")
+
+
+def test_patched_scaled_mm_vs_torch_cpu(dev):
+    g = gen(25)
+    x = torch.randn(256, 1024, generator=g)
+    sa = x.abs().amax() / 448
+    a = (x / sa).clamp(-448, 448).to(torch.float8_e4m3fn)
+    wf = 0.02 * torch.randn(512, 1024, generator=g)
+    sb = wf.abs().amax() / 448
+    w = (wf / sb).clamp(-448, 448).to(torch.float8_e4m3fn)
+    ref = torch._scaled_mm(a, w.t(), scale_a=sa, scale_b=sb, out_dtype=torch.bfloat16)
+    assert scaled_mm_fp8.install()
+    try:
+        out = torch._scaled_mm(a.to(dev), w.to(dev).t(), scale_a=sa.to(dev), scale_b=sb.to(dev),
+                               out_dtype=torch.bfloat16)
+    finally:
+        scaled_mm_fp8.uninstall()
+    assert_close(bf16_to_f32(bits16(out)), ref.float().numpy(), "patched _scaled_mm")
+
+
+@pytest.mark.parametrize("scaled", [False, True])
+def test_w8a16_forward_vs_oracle(dev, scaled):
+    g = gen(26)
+    N, K = 768, 1024
+    wf = 0.02 * torch.randn(N, K, generator=g)
+    ws = wf.abs().amax() / 448 if scaled else None
+    w = ((wf / ws) if scaled else wf * 20).clamp(-448, 448).to(torch.float8_e4m3fn)
+    bias = (0.01 * torch.randn(N, generator=g)).to(torch.bfloat16)
+    layer = types.SimpleNamespace(
+        weight=torch.nn.Parameter(w.to(dev), requires_grad=False), bias=bias.to(dev),
+        weight_function=[], bias_function=[])
+    if scaled:
+        layer.scale_weight = ws.reshape(()).to(dev)
+    x = torch.randn(3, 100, K, generator=g).to(torch.bfloat16)
+    assert linear_fp8_w8a16._eligible(layer, x.to(dev))
+    linear_fp8_w8a16._self_checked = False
+    out = linear_fp8_w8a16._w8a16_forward(layer, x.to(dev))
+    assert out.shape == (3, 100, N) and out.dtype == torch.bfloat16
+    ref = of.w8a16_linear(bits16(x.reshape(-1, K)), u8(w), ws.reshape(1).numpy() if scaled else None,
+                          bias.float().numpy(), "f32")
+    assert_close(bf16_to_f32(bits16(out.reshape(-1, N))), bf16_to_f32(ref), "w8a16 forward")
+
+
+def test_krea2_project_exact(dev):
+    g = gen(27)
+    x = torch.randn(1, 200, 512, generator=g).to(torch.bfloat16)
+    wg, wu = _i8((384, 512), g), _i8((384, 512), g)
+    gs, us = torch.rand(384, generator=g) * 0.02, torch.rand(384, generator=g) * 0.02
+    int8_linear._act_cache = None
+    out = krea2_ffn_pair.project(x.to(dev), (wg.to(dev), gs.to(dev)), (wu.to(dev), us.to(dev)))
+    assert out.shape == (1, 200, 384)
+    # the unfused chain with the same device's bf16 SiLU (table of F.silu on dev)
+    q, rs = oi.quant_rowwise(bits16(x.reshape(-1, 512)))
+    gb = oi.epilogue_rowcolscale(oi.i8_matmul2d_nt(q, wg.numpy()), rs, gs.numpy())
+    ub = oi.epilogue_rowcolscale(oi.i8_matmul2d_nt(q, wu.numpy()), rs, us.numpy())
+    silu_dev = ops.act_table("silu", dev).cpu().numpy().view(np.uint16)
+    act = oact.apply_table(silu_dev, gb)
+    ref = bits16(torch.from_numpy(bf16_to_f32(act) * bf16_to_f32(ub)).to(torch.bfloat16))
+    assert_bits_equal(bits16(out.reshape(-1, 384)), ref, "krea2 project")
+
+
+def test_moss_project_exact(dev):
+    g = gen(28)
+    q, w = _i8((130, 384), g), _i8((2 * 256, 384), g)
+    rs, cs = torch.rand(130, generator=g) * 0.01, torch.rand(512, generator=g) * 0.02
+    th, tg = oact.situ_tables()
+    tabs = tuple(torch.from_numpy(t.view(np.int16)).to(dev) for t in (th, tg))
+    out = moss_ffn.project(q.to(dev), rs.to(dev), w.to(dev), cs.to(dev), tabs)
+    ref = op.moss_pair(q.numpy(), w.numpy(), rs.numpy(), cs.numpy(), th, tg)
+    assert_bits_equal(bits16(out), ref, "moss project")
