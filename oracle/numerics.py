@@ -36,8 +36,10 @@ def bf16_round(x):
 
 
 def f32_to_f16_bits(x):
-    """float32 -> IEEE half bits, RNE (numpy's astype is RNE)."""
-    return np.asarray(x, dtype=F32).astype(np.float16).view(np.uint16)
+    """float32 -> IEEE half bits, RNE (numpy's astype is RNE); values past the
+    half range become +-inf, as in torch."""
+    with np.errstate(over="ignore"):
+        return np.asarray(x, dtype=F32).astype(np.float16).view(np.uint16)
 
 
 def f16_bits_to_f32(h):

@@ -105,6 +105,24 @@ def test_i8_fused_cs_exact(dev, M, K, N, bias):
     assert_bits_equal(bits16(d), ref, f"fused_cs {M}x{K}x{N}")
 
 
+def test_c1_golden_digest_full_size(dev):
+    """BASELINE C1 at full size (seed 1): the kernel's INT32 product and
+    per-channel bf16 epilogue hash to the digests written from torch._int_mm
+    and torch's eager epilogue by tests/golden/make_golden.py."""
+    import hashlib, json, pathlib
+    d = json.loads((pathlib.Path(__file__).parent / "golden" / "digests.json").read_text())
+    g = gen(d["c1_seed"])
+    M, K, N = 1024, 3072, 3072
+    x = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8)
+    w = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
+    rs = 0.005 + 0.015 * torch.rand(M, generator=g)
+    cs = 0.0005 + 0.0015 * torch.rand(N, generator=g)
+    c = ops.i8_matmul2d_nt(x.to(dev), w.to(dev)).cpu().numpy()
+    assert hashlib.sha256(c.tobytes()).hexdigest() == d["c1_int32_sha256"]
+    e = ops.i8_matmul2d_nt_fused_cs(x.to(dev), w.to(dev), rs.to(dev), cs.to(dev))
+    assert hashlib.sha256(bits16(e).view(np.int16).tobytes()).hexdigest() == d["c1_epilogue_bf16_sha256"]
+
+
 def test_c1_config_exact(dev):
     """X, W int8 uniform in [-127,127] (seed 1),
     rs U[0.005,0.02] [1024], cs U[0.0005,0.002] [3072]."""
