@@ -311,6 +311,73 @@ def bench_c5(torch, ops, dev, steps, warmup):
     return res
 
 
+# ------------------------------------------------------------- traffic ---
+# HBM traffic of the headline kernel from two rocprofv3 counter passes over
+# `bench.py --pmc-target` (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch).
+# The same run first copies COPY_BYTES with a plain device copy; the factor
+# algorithmic bytes / counted bytes of that copy calibrates each counter.
+# `bench.py --pmc-summarize FETCH_DIR WRITE_DIR` writes TRAFFIC_FILE, which
+# the default run reports as roofline.traffic.
+COPY_BYTES = 512 * 1024 * 1024
+TRAFFIC_FILE = ROOT / "profiles" / "w8a16_gemm_c2_qkv_traffic.json"
+QKV_KERNEL_KEY = "OpW8A16"
+
+
+def pmc_target(torch, ops, dev):
+    src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=dev).uniform_()
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    x, layers = make_c2(torch, dev)
+    q, s, b = layers[0]
+    for _ in range(3):
+        ops.w8a16_linear(x, q, s, b)
+    torch.cuda.synchronize()
+
+
+def _pmc_rows(d, counter):
+    import csv
+    rows = []
+    for f in pathlib.Path(d).rglob("*counter_collection.csv"):
+        for r in csv.DictReader(open(f)):
+            if r["Counter_Name"] == counter:
+                rows.append((int(r.get("Dispatch_Id", 0) or 0), r["Kernel_Name"], float(r["Counter_Value"])))
+    rows.sort()
+    return rows
+
+
+def pmc_summarize(fetch_dir, write_dir):
+    out = {}
+    for counter, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
+        rows = _pmc_rows(d, counter)
+        copies = [v for _, k, v in rows if "copyBuffer" in k]      # dst.copy_(src): the runtime's blit
+        qkv = [v for _, k, v in rows if "gemm_tile_kernel" in k and QKV_KERNEL_KEY in k]
+        if not copies or not qkv:
+            raise SystemExit(f"{counter}: copy or QKV dispatches not found in {d}")
+        copy_kib = statistics.median(copies[-3:])
+        factor = (COPY_BYTES / 1024.0) / copy_kib
+        kib = statistics.median(qkv)
+        out[counter] = {"copy_kib_per_dispatch": copy_kib, "factor": factor,
+                        "qkv_kib_per_dispatch": kib, "qkv_bytes": kib * 1024.0 * factor}
+    M, K, N = 9216, 3072, 9216
+    algo = M * K * 2 + N * K + N * 2 + 4 + M * N * 2   # X bf16 + W fp8 + bias bf16 + scale + Y bf16
+    out["traffic_bytes"] = out["FETCH_SIZE"]["qkv_bytes"] + out["WRITE_SIZE"]["qkv_bytes"]
+    out["algorithmic_bytes"] = algo
+    out["kernel"] = "W8A16 GEMM fused-QKV 9216x3072 -> 9216 (C2)"
+    TRAFFIC_FILE.write_text(json.dumps(out, indent=1) + "\n")
+    print(json.dumps(out))
+
+
+def load_traffic():
+    try:
+        t = json.loads(TRAFFIC_FILE.read_text())
+        return round(t["traffic_bytes"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -319,7 +386,14 @@ def main():
     ap.add_argument("--only", default="C1,C2,C3,C4,C5",
                     help="comma list of configs to run (C2 is always run)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--pmc-target", action="store_true",
+                    help="run the copy calibration and the C2 QKV kernel for rocprofv3 --pmc")
+    ap.add_argument("--pmc-summarize", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="write the traffic summary from two rocprofv3 --pmc output dirs")
     args = ap.parse_args()
+    if args.pmc_summarize:
+        pmc_summarize(*args.pmc_summarize)
+        return
     if args.gpus != 1:
         log(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
             "(multi-GPU sharding is design-only).")
@@ -330,6 +404,9 @@ def main():
     import cdna4q.ops as ops
 
     dev = torch.device("cuda", 0)
+    if args.pmc_target:
+        pmc_target(torch, ops, dev)
+        return
     only = {c.strip().upper() for c in args.only.split(",") if c.strip()}
     per = {}
     log("C2 (headline) ...")
@@ -370,7 +447,8 @@ def main():
                    "M": 9216, "K": 3072, "N": [9216, 3072]},
         "roofline": {"bound": "mfma", "achieved": round(kt, 2) if kt else None,
                      "peak": PEAK["bf16"], "unit": "TFLOP/s",
-                     "frac": round(kt / PEAK["bf16"], 4) if kt else None, "traffic": None,
+                     "frac": round(kt / PEAK["bf16"], 4) if kt else None,
+                     "traffic": load_traffic(),
                      "kernel": c2["kernel"]},
         "cpu_baseline": cpu,
         "per_config": per,
