@@ -658,6 +658,10 @@ gemm_tile_kernel(GemmShape sh, Src2 sa, Src2 sb, const float* b_scale, Epi epi) 
           if (st + 1 < nst) Op::template frags<TM, TN>(fr[0], nxt, nxt + BM * SA, ra0, rb0i, 0);
         } else {
           Op::template frags<TM, TN>(fr[(s + 1) & 1], cur, cur + BM * SA, ra0, rb0i, s + 1);
+          // keep the next step's LDS reads ahead of this step's MFMAs: left to
+          // the scheduler they sink behind most of them, and the LDS latency
+          // then lands on the stage barrier (2-4% on the large shapes)
+          __builtin_amdgcn_sched_barrier(0);
         }
         Op::template mma<TM, TN>(fr[s & 1], acc, ws);
       }
