@@ -14,13 +14,10 @@ template <bool BF16, bool HAS_SCALE, class Epi>
 int run_w8a16_tiled(const uint16_t* a, int64_t lda, const uint8_t* w, int64_t ldw,
                     const float* w_scale, int64_t M, int64_t N, int64_t K, const Epi& epi,
                     hipStream_t s, const char* what) {
-  GemmShape sh{M, N, K, 0, 0};
   const Src2 sa{reinterpret_cast<const uint8_t*>(a), reinterpret_cast<const uint8_t*>(a), 2 * lda, M};
   const Src2 sb{w, w, ldw, N};
-  return with_tile(pick_tile(M, N), [&](auto t) {
-    using T = decltype(t);
-    return launch_tile<T, OpW8A16<BF16, HAS_SCALE>, false>(sh, N, sa, sb, w_scale, epi, s, what);
-  });
+  return run_tiles<false>(M, N, N, K, sa, sb, w_scale, epi, s, what,
+                          [](auto) { return OpW8A16<BF16, HAS_SCALE>{}; });
 }
 
 }  // namespace

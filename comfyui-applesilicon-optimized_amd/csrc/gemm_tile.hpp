@@ -306,17 +306,47 @@ struct TileCoord { int tm, tn; };
 // Remap the dispatch order (blocks go round-robin over the 8 XCDs) so each
 // XCD owns a contiguous run of tiles, then raster that run in bands of
 // kGroupM tile rows.
-__device__ __forceinline__ TileCoord tile_of(int bid, int nblocks, int tiles_m, int tiles_n) {
+__host__ __device__ inline TileCoord tile_of(int bid, int nblocks, int tiles_m, int tiles_n) {
   const int full = nblocks & ~7;
   if (bid < full) bid = (bid & 7) * (full >> 3) + (bid >> 3);
   const int band = kGroupM * tiles_n;
   const int first_m = (bid / band) * kGroupM;
-  const int gm = min(tiles_m - first_m, kGroupM);
+  const int gm = tiles_m - first_m < kGroupM ? tiles_m - first_m : kGroupM;
   const int in_band = bid - (bid / band) * band;
   TileCoord t;
   t.tm = first_m + in_band % gm;
   t.tn = in_band / gm;
   return t;
+}
+
+// A launch covers `count` kernel tiles: mapped tiles first, first+1, ... of
+// the tiles_m x tiles_n grid (in tile_of order), each split into sub_m x
+// sub_n kernel tiles (1 x 1: the kernel tile is the mapped tile). A large
+// GEMM runs its whole rounds of big tiles in one launch and the leftover
+// mapped tiles, split, in a second launch of a smaller tile, so that the
+// leftover work spreads over every CU.
+struct GemmShape {
+  int64_t M, N, K;          // N = output columns (pair kernels: 2 * N_out)
+  int tiles_m, tiles_n;     // grid of mapped tiles
+  int first, count;
+  int sub_m, sub_n;
+};
+
+// Kernel tile i of a launch, in kernel-tile units. Split tiles: the
+// dispatch-order remap of tile_of first gives each XCD a contiguous run of
+// kernel tiles, so the pieces of one mapped tile share an L2.
+__host__ __device__ inline TileCoord tile_at(const GemmShape& sh, int i) {
+  const int nmapped = sh.tiles_m * sh.tiles_n;
+  if (sh.sub_m == 1 && sh.sub_n == 1) return tile_of(sh.first + i, nmapped, sh.tiles_m, sh.tiles_n);
+  const int full = sh.count & ~7;
+  if (i < full) i = (i & 7) * (full >> 3) + (i >> 3);
+  const int per = sh.sub_m * sh.sub_n;
+  const int t = i / per, s = i - t * per;
+  const TileCoord b = tile_of(sh.first + t, nmapped, sh.tiles_m, sh.tiles_n);
+  TileCoord r;
+  r.tm = b.tm * sh.sub_m + s / sh.sub_n;
+  r.tn = b.tn * sh.sub_n + s % sh.sub_n;
+  return r;
 }
 
 // ------------------------------------------------------------ epilogue ---
@@ -511,10 +541,6 @@ __device__ __forceinline__ void epilogue_pair(const Acc (&acc)[TM][TN], int64_t 
 }
 
 // --------------------------------------------------------- main kernel ---
-struct GemmShape {
-  int64_t M, N, K;          // N = output columns (pair kernels: 2 * N_out)
-  int tiles_m, tiles_n;
-};
 
 // Operand sources: base pointers and strides; each workgroup derives its
 // tiles' buffer resources from them.
@@ -572,7 +598,7 @@ gemm_tile_kernel(GemmShape sh, Src2 sa, Src2 sb, const float* b_scale, Epi epi) 
   static_assert((NBUF - 1) * kPerStage < 64, "too many copies in flight for vmcnt");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[RING + kStrip * WM * WN];
 
-  const int ntiles = sh.tiles_m * sh.tiles_n;
+  const int ntiles = sh.count;
   const int G = (int)gridDim.x;
   const int my_tiles = (ntiles - 1 - (int)blockIdx.x) / G + 1;
   const Epi ep = epi.prepare();
@@ -592,7 +618,7 @@ gemm_tile_kernel(GemmShape sh, Src2 sa, Src2 sb, const float* b_scale, Epi epi) 
   int ij = 0, ips = 0;
   __amdgpu_buffer_rsrc_t ra, rb0, rb1;
   auto tile_rsrc = [&](int j) {
-    const TileCoord tc = tile_of((int)blockIdx.x + j * G, ntiles, sh.tiles_m, sh.tiles_n);
+    const TileCoord tc = tile_at(sh, (int)blockIdx.x + j * G);
     const int64_t m0 = (int64_t)tc.tm * BM;
     const int64_t brow0 = PAIR ? ((int64_t)tc.tn * BN >> 1) : (int64_t)tc.tn * BN;
     const int64_t bleft = (sb.rows - brow0) * sb.ld_bytes;
@@ -666,7 +692,7 @@ gemm_tile_kernel(GemmShape sh, Src2 sa, Src2 sb, const float* b_scale, Epi epi) 
         Op::template mma<TM, TN>(fr[s & 1], acc, ws);
       }
     }
-    const TileCoord tc = tile_of((int)blockIdx.x + j * G, ntiles, sh.tiles_m, sh.tiles_n);
+    const TileCoord tc = tile_at(sh, (int)blockIdx.x + j * G);
     const int64_t wm0 = (int64_t)tc.tm * BM + wm * (TM * 32);
     if constexpr (PAIR) {
       const int64_t c0 = ((int64_t)tc.tn * BN >> 1) + wn * (TN * 16);

@@ -87,12 +87,9 @@ extern "C" int c4q_i8_ffn_pair(const int8_t* a, int64_t lda, const int8_t* w_gat
                        N_out, K, nbx, a, lda, w_gate, w_up, ldw, epi);
     return check_launch(what);
   }
-  GemmShape sh{M, 2 * N_out, K, 0, 0};
   const Src2 sa{reinterpret_cast<const uint8_t*>(a), reinterpret_cast<const uint8_t*>(a), lda, M};
   const Src2 sb{reinterpret_cast<const uint8_t*>(w_gate), reinterpret_cast<const uint8_t*>(w_up),
                 ldw, N_out};
-  return with_tile(pick_tile(M, 2 * N_out), [&](auto t) {
-    using T = decltype(t);
-    return launch_tile<T, OpI8T<T::KS8>, true>(sh, 2 * N_out, sa, sb, nullptr, epi, s, what);
-  });
+  return run_tiles<true>(M, 2 * N_out, 2 * N_out, K, sa, sb, nullptr, epi, s, what,
+                         [](auto t) { return OpI8T<decltype(t)::KS8>{}; });
 }

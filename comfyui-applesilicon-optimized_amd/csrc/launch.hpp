@@ -53,36 +53,6 @@ int with_tile(int id, F&& f) {
   }
 }
 
-// Tile choice by a cost model of the persistent kernel: a tile variant runs
-// in ceil(tiles / slots) rounds (slots = CUs x resident workgroups per CU),
-// each costing one tile's MACs times the slots it fills, at the variant's
-// measured relative per-CU throughput on large shapes (MI355X, 8-bit
-// operands: 256x256 w8 1.00, 256x256 w4 0.90, 128x128 0.87, 64x128 0.70).
-// A tile id in the environment variable C4Q_TILE (0..6) overrides it, for
-// tuning sweeps.
-inline int pick_tile(int64_t M, int64_t N) {
-  const char* env = getenv("C4Q_TILE");
-  if (env && env[0] >= '0' && env[0] < '0' + TILE_COUNT && env[1] == 0) return env[0] - '0';
-  struct Cand { int id, bm, bn, per_cu; double eff; };
-  static const Cand cands[] = {{TILE_256x256_W8, 256, 256, 1, 1.00},
-                               {TILE_128x128_W4_K128, 128, 128, 2, 0.87},
-                               {TILE_64x128_W4_K128, 64, 128, 2, 0.70}};
-  const double cus = 256;
-  int best = TILE_256x256_W8;
-  double best_cost = 0;
-  for (const Cand& c : cands) {
-    const double tiles = (double)(cdiv(M, c.bm) * cdiv(N, c.bn));
-    const double slots = cus * c.per_cu;
-    const double rounds = (double)(int64_t)((tiles + slots - 1) / slots);
-    const double cost = rounds * slots * c.bm * c.bn / c.eff;
-    if (c.id == TILE_256x256_W8 || cost < best_cost) {
-      best = c.id;
-      best_cost = cost;
-    }
-  }
-  return best;
-}
-
 // Compute units of the current device (cached per device id).
 int device_cus();
 
@@ -103,19 +73,124 @@ int persistent_grid(K kernel, int nt, int64_t tiles, int& occ) {
 }
 
 template <class T, class Op, bool PAIR, class Epi>
-int launch_tile(GemmShape sh, int64_t n_rows_b, const Src2& sa, const Src2& sb, const float* b_scale,
+int launch_tile(const GemmShape& sh, const Src2& sa, const Src2& sb, const float* b_scale,
                 const Epi& epi, hipStream_t s, const char* what) {
-  sh.tiles_m = (int)cdiv(sh.M, T::BM);
-  sh.tiles_n = (int)cdiv(n_rows_b, T::BN);
-  const int64_t tiles = (int64_t)sh.tiles_m * sh.tiles_n;
-  C4Q_REQUIRE(tiles < (1ll << 30), C4Q_ERR_SHAPE, "%s: problem too large (%lld tiles)", what,
-              (long long)tiles);
   constexpr int nbuf = ring_depth<T, Op, PAIR>();
   auto kernel = gemm_tile_kernel<Op, T::BM, T::BN, T::WM, T::WN, nbuf, PAIR, Epi>;
   static int occ = 0;
-  const int grid = persistent_grid(kernel, T::NT, tiles, occ);
+  const int grid = persistent_grid(kernel, T::NT, sh.count, occ);
   hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(T::NT), 0, s, sh, sa, sb, b_scale, epi);
   return check_launch(what);
+}
+
+// Tile plan of one GEMM: the main tile variant and how many of its tiles
+// (in tile_of order) the main launch takes; with a tail variant, the rest of
+// the tiles are split into pieces of that variant in a second launch.
+struct TilePlan {
+  int main_id;
+  int64_t main_count;
+  int tail_id;              // < 0: no tail launch
+};
+
+inline int tile_bm(int id) { return with_tile(id, [](auto t) { return decltype(t)::BM; }); }
+inline int tile_bn(int id) { return with_tile(id, [](auto t) { return decltype(t)::BN; }); }
+
+// Cost model of the persistent kernel in CU-time units (one unit: the K MACs
+// of one output element at the big tile's per-CU rate). A variant runs its
+// tiles in rounds of `slots` (CUs x resident workgroups); a round costs the
+// tile area x workgroups per CU / the variant's relative per-CU throughput,
+// measured on large shapes (MI355X, 8-bit operands: 256x256 1.00, 128x128
+// 0.87, 64x128 0.70). When the big tile's last round would leave CUs idle,
+// its whole rounds can run as one launch and the leftover tiles, split into
+// pieces of a smaller variant, as a second launch spread over every CU; the
+// second launch costs about 3 us more (9e6 / K units at ~6 TOP/s per CU).
+// A tile id in the environment variable C4Q_TILE (0..6) forces one launch
+// of that variant, for tuning sweeps.
+inline TilePlan plan_tiles(int64_t M, int64_t N, int64_t K, int cus) {
+  const char* env = getenv("C4Q_TILE");
+  if (env && env[0] >= '0' && env[0] < '0' + TILE_COUNT && env[1] == 0) {
+    const int id = env[0] - '0';
+    return {id, cdiv(M, tile_bm(id)) * cdiv(N, tile_bn(id)), -1};
+  }
+  struct Cand { int id, per_cu; double eff; };
+  static const Cand cands[] = {{TILE_256x256_W8, 1, 1.00},
+                               {TILE_128x128_W4_K128, 2, 0.87},
+                               {TILE_64x128_W4_K128, 2, 0.70}};
+  const double gap = 9e6 / (double)(K > 0 ? K : 1);
+  TilePlan best{TILE_256x256_W8, 0, -1};
+  double best_cost = -1;
+  for (const Cand& c : cands) {
+    const int bm = tile_bm(c.id), bn = tile_bn(c.id);
+    const int64_t tiles = cdiv(M, bm) * cdiv(N, bn);
+    const int64_t slots = (int64_t)cus * c.per_cu;
+    const double round = (double)c.per_cu * bm * bn / c.eff;
+    const double plain = (double)cdiv(tiles, slots) * round;
+    if (best_cost < 0 || plain < best_cost) {
+      best = {c.id, tiles, -1};
+      best_cost = plain;
+    }
+    const int64_t whole = tiles / slots * slots, rest = tiles - whole;
+    if (whole == 0 || rest == 0) continue;
+    for (const Cand& t : cands) {
+      const int tm = tile_bm(t.id), tn = tile_bn(t.id);
+      if (tm * tn >= bm * bn || bm % tm || bn % tn) continue;
+      const int64_t pieces = rest * (bm / tm) * (bn / tn);
+      const int64_t tslots = (int64_t)cus * t.per_cu;
+      const double cost = (double)(whole / slots) * round +
+                          (double)cdiv(pieces, tslots) * t.per_cu * tm * tn / t.eff + gap;
+      if (cost < best_cost) {
+        best = {c.id, whole, t.id};
+        best_cost = cost;
+      }
+    }
+  }
+  return best;
+}
+
+// The launches of a GEMM's tile plan as (tile id, shape) pairs; returns
+// their number (1 or 2). n_rows_b = rows of the B tile space (pair kernels:
+// 2 * N_out), N = output columns.
+inline int plan_launches(int64_t M, int64_t n_rows_b, int64_t N, int64_t K, int cus, int ids[2],
+                         GemmShape shs[2]) {
+  const TilePlan p = plan_tiles(M, n_rows_b, K, cus);
+  const int bm = tile_bm(p.main_id), bn = tile_bn(p.main_id);
+  const int64_t mapped = cdiv(M, bm) * cdiv(n_rows_b, bn);
+  GemmShape sh{M, N, K, (int)cdiv(M, bm), (int)cdiv(n_rows_b, bn), 0, (int)p.main_count, 1, 1};
+  int n = 0;
+  if (sh.count > 0) {
+    ids[n] = p.main_id;
+    shs[n++] = sh;
+  }
+  if (p.tail_id >= 0) {
+    sh.first = (int)p.main_count;
+    sh.sub_m = bm / tile_bm(p.tail_id);
+    sh.sub_n = bn / tile_bn(p.tail_id);
+    sh.count = (int)((mapped - p.main_count) * sh.sub_m * sh.sub_n);
+    ids[n] = p.tail_id;
+    shs[n++] = sh;
+  }
+  return n;
+}
+
+// Runs a GEMM through its tile plan. OpFor maps a Tile to its operand policy
+// (a callable whose return type is the policy).
+template <bool PAIR, class OpFor, class Epi>
+int run_tiles(int64_t M, int64_t n_rows_b, int64_t N, int64_t K, const Src2& sa, const Src2& sb,
+              const float* b_scale, const Epi& epi, hipStream_t s, const char* what, OpFor op_for) {
+  // bound on the tile count of any plan (the smallest tile is 64 x 128)
+  C4Q_REQUIRE(cdiv(M, 64) * cdiv(n_rows_b, 128) < (1ll << 27), C4Q_ERR_SHAPE,
+              "%s: problem too large (%lld x %lld)", what, (long long)M, (long long)n_rows_b);
+  int ids[2];
+  GemmShape shs[2];
+  const int n = plan_launches(M, n_rows_b, N, K, device_cus(), ids, shs);
+  for (int l = 0; l < n; ++l) {
+    const int st = with_tile(ids[l], [&](auto t) {
+      using T = decltype(t);
+      return launch_tile<T, decltype(op_for(t)), PAIR>(shs[l], sa, sb, b_scale, epi, s, what);
+    });
+    if (st != C4Q_OK) return st;
+  }
+  return C4Q_OK;
 }
 
 template <class Op, class Epi>
@@ -144,12 +219,9 @@ int run_gemm8(const uint8_t* a, int64_t lda, const uint8_t* b, int64_t ldb, int6
   const bool tiled = K > 0 && K % 16 == 0 && aligned16(a) && aligned16(b) && lda % 16 == 0 &&
                      ldb % 16 == 0 && tile_offsets_fit(lda, ldb);
   if (!tiled) return launch_generic(M, N, K, GenOp::make(a, lda, b, ldb), epi, s, what);
-  GemmShape sh{M, N, K, 0, 0};
   const Src2 sa{a, a, lda, M}, sb{b, b, ldb, N};
-  return with_tile(pick_tile(M, N), [&](auto t) {
-    using T = decltype(t);
-    return launch_tile<T, OpT<T::KS8>, false>(sh, N, sa, sb, nullptr, epi, s, what);
-  });
+  return run_tiles<false>(M, N, N, K, sa, sb, nullptr, epi, s, what,
+                          [](auto t) { return OpT<decltype(t)::KS8>{}; });
 }
 
 }  // namespace c4q

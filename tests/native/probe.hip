@@ -1,9 +1,11 @@
-// Test-only probes of gfx950 conversion instructions, checked exhaustively
-// against the library's integer-only reference roundings (numerics.hpp).
+// Test-only probes: gfx950 conversion instructions, checked exhaustively
+// against the library's integer-only reference roundings (numerics.hpp), and
+// the host-side tile planning of the GEMM launches (launch.hpp).
 // Built into tests/native/libc4q_probe.so; used by tests/test_gpu_numerics.py.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "launch.hpp"
 #include "numerics.hpp"
 
 using namespace c4q;
@@ -51,4 +53,41 @@ extern "C" int c4q_probe_cvt_exhaustive(int which, unsigned long long* out, void
   if (which == 0) hipLaunchKernelGGL(cvt_bf16_all, grid, block, 0, s, out, first);
   else hipLaunchKernelGGL(cvt_f16_all, grid, block, 0, s, out, first);
   return (int)hipGetLastError();
+}
+
+// ---------------------------------------------------------- tile plans ---
+// Host-side enumeration of the launches a GEMM's tile plan issues
+// (plan_launches, tile_at -- the functions the library runs). cover
+// [cdiv(M, 64) * cdiv(n_rows_b, 128)] counts, per 64 x 128 output cell
+// inside the matrix, the kernel tiles that compute it (every tile size is a
+// multiple of the cell). info[8]: launches, then (tile id, kernel tiles) of
+// each launch, then the main launch's first and the tail launch's sub_m,
+// sub_n. Returns 0, or -1 if cover_len is too small.
+extern "C" int c4q_probe_tile_plan(int64_t M, int64_t n_rows_b, int64_t K, int cus, int32_t* cover,
+                                   int64_t cover_len, int64_t* info) {
+  const int64_t cm = cdiv(M, 64), cn = cdiv(n_rows_b, 128);
+  if (cm * cn > cover_len) return -1;
+  for (int64_t i = 0; i < cm * cn; ++i) cover[i] = 0;
+  int ids[2];
+  GemmShape shs[2];
+  const int n = plan_launches(M, n_rows_b, n_rows_b, K, cus, ids, shs);
+  for (int k = 0; k < 8; ++k) info[k] = 0;
+  info[0] = n;
+  for (int l = 0; l < n; ++l) {
+    const int bm = tile_bm(ids[l]), bn = tile_bn(ids[l]);
+    info[1 + 2 * l] = ids[l];
+    info[2 + 2 * l] = shs[l].count;
+    if (l == 1) {
+      info[6] = shs[l].sub_m;
+      info[7] = shs[l].sub_n;
+    }
+    for (int i = 0; i < shs[l].count; ++i) {
+      const TileCoord t = tile_at(shs[l], i);
+      for (int64_t r = (int64_t)t.tm * bm; r < (int64_t)(t.tm + 1) * bm; r += 64)
+        for (int64_t c = (int64_t)t.tn * bn; c < (int64_t)(t.tn + 1) * bn; c += 128)
+          if (r < M && c < n_rows_b) ++cover[(r / 64) * cn + c / 128];
+    }
+  }
+  info[5] = n ? shs[0].first : 0;
+  return 0;
 }

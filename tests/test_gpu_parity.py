@@ -419,3 +419,95 @@ def test_every_tile_variant(dev, monkeypatch, tile):
     y = ops.w8a16_linear(x.to(dev), wf.to(dev), ws.to(dev), bb.to(dev))
     ref = of.w8a16_linear(bits16(x), u8(wf), ws.numpy(), bits16(bb))
     assert_close(bf16_to_f32(bits16(y)), bf16_to_f32(ref), f"tile {tile} w8a16")
+
+
+# ------------------------------------------------------ split tile plans ---
+# Shapes whose last round of 256x256 tiles would leave most CUs idle: the
+# library runs the whole rounds as one launch and splits the leftover tiles
+# into 64x128 or 128x128 pieces run by a second launch. Each case is checked
+# against the oracle and, bit for bit, against the single-launch plan
+# (C4Q_TILE=0): every output element accumulates its K products in the same
+# order in every tile variant.
+
+def _device_plan(M, n_rows_b, K):
+    import ctypes, pathlib
+    lib = ctypes.CDLL(str(pathlib.Path(__file__).resolve().parent / "native" / "libc4q_probe.so"))
+    f = lib.c4q_probe_tile_plan
+    f.argtypes = [ctypes.c_int64] * 3 + [ctypes.c_int, ctypes.c_void_p, ctypes.c_int64,
+                                         ctypes.c_void_p]
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    cover = np.zeros(-(-M // 64) * -(-n_rows_b // 128), np.int32)
+    info = np.zeros(8, np.int64)
+    assert f(M, n_rows_b, K, cus, cover.ctypes.data, cover.size, info.ctypes.data) == 0
+    if info[0] != 2:
+        pytest.skip(f"no split plan for {M}x{n_rows_b} on {cus} CUs")
+    return info
+
+
+SPLIT_CASES = [(4352, 512, 4352), (4312, 1040, 4280), (4608, 1024, 4608)]   # 64x128, 64x128, 128x128 pieces
+
+
+@pytest.mark.parametrize("M,K,N", SPLIT_CASES)
+def test_split_plan_int8_exact(dev, monkeypatch, M, K, N):
+    _device_plan(M, N, K)
+    g = gen(M + K + N)
+    a, b = _randint8((M, K), g), _randint8((N, K), g)
+    rs = torch.rand(M, generator=g) * 0.01
+    cs = torch.rand(N, generator=g) * 0.02
+    bb = torch.randn(N, generator=g).to(torch.bfloat16)
+    ad, bd = a.to(dev), b.to(dev)
+    c = ops.i8_matmul2d_nt(ad, bd).cpu().numpy()
+    d = bits16(ops.i8_matmul2d_nt_fused_cs(ad, bd, rs.to(dev), cs.to(dev), bb.to(dev)))
+    ref_c = oi.i8_matmul2d_nt(a.numpy(), b.numpy())
+    assert_bits_equal(c, ref_c, f"split int32 {M}x{K}x{N}")
+    assert_bits_equal(d, oi.epilogue_rowcolscale(ref_c, rs.numpy(), cs.numpy(), bits16(bb)),
+                      f"split fused_cs {M}x{K}x{N}")
+    monkeypatch.setenv("C4Q_TILE", "0")
+    d1 = bits16(ops.i8_matmul2d_nt_fused_cs(ad, bd, rs.to(dev), cs.to(dev), bb.to(dev)))
+    assert_bits_equal(d, d1, "split plan vs one launch")
+
+
+def test_split_plan_pair_exact(dev, monkeypatch):
+    M, K, N_out = 4352, 512, 2176
+    _device_plan(M, 2 * N_out, K)
+    g = gen(77)
+    a, wg, wu = _randint8((M, K), g), _randint8((N_out, K), g), _randint8((N_out, K), g)
+    rs = torch.rand(M, generator=g) * 0.01
+    gs = torch.rand(N_out, generator=g) * 0.02
+    us = torch.rand(N_out, generator=g) * 0.02
+    silu = torch.from_numpy(oact.silu_table().view(np.int16))
+    args = (a.to(dev), wg.to(dev), wu.to(dev), rs.to(dev), gs.to(dev), us.to(dev), silu.to(dev), None)
+    p = bits16(ops.ffn_pair(*args))
+    assert_bits_equal(p, op.krea2_pair(a.numpy(), wg.numpy(), wu.numpy(), rs.numpy(), gs.numpy(),
+                                       us.numpy()), "split pair")
+    monkeypatch.setenv("C4Q_TILE", "0")
+    assert_bits_equal(p, bits16(ops.ffn_pair(*args)), "split pair vs one launch")
+
+
+@pytest.mark.parametrize("M,K,N", SPLIT_CASES)
+def test_split_plan_fp8_and_w8a16(dev, monkeypatch, M, K, N):
+    _device_plan(M, N, K)
+    g = gen(5 * M + N)
+    af = _fp8(torch.randn(M, K, generator=g))
+    wf = _fp8(torch.randn(N, K, generator=g) * 0.1)
+    sa, sb = torch.tensor(0.7), torch.tensor(1.3)
+    bb = torch.randn(N, generator=g).to(torch.bfloat16)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    ws = (wf.float().abs().amax() / 448).reshape(1)
+    afd, wfd, xd = af.to(dev), wf.to(dev), x.to(dev)
+
+    def run():
+        o = ops.scaled_mm(afd, wfd.t(), out_dtype=torch.bfloat16, scale_a=sa.to(dev),
+                          scale_b=sb.to(dev))
+        y = ops.w8a16_linear(xd, wfd, ws.to(dev), bb.to(dev))
+        return bits16(o), bits16(y)
+
+    o, y = run()
+    assert_close(bf16_to_f32(o), bf16_to_f32(of.scaled_mm(u8(af), u8(wf), sa.numpy(), sb.numpy())),
+                 f"split fp8 {M}x{K}x{N}")
+    assert_close(bf16_to_f32(y), bf16_to_f32(of.w8a16_linear(bits16(x), u8(wf), ws.numpy(), bits16(bb))),
+                 f"split w8a16 {M}x{K}x{N}")
+    monkeypatch.setenv("C4Q_TILE", "0")
+    o1, y1 = run()
+    assert_bits_equal(o, o1, "split fp8 vs one launch")
+    assert_bits_equal(y, y1, "split w8a16 vs one launch")

@@ -1,0 +1,103 @@
+"""Tile plans of the MFMA GEMM launches, run on the host (no GPU).
+
+A GEMM whose last round of big tiles would leave most CUs idle runs its
+whole rounds as one launch and the leftover tiles, split into smaller
+pieces, as a second launch. tests/native/libc4q_probe.so exposes the
+library's own planning and tile-mapping functions (plan_launches, tile_at);
+these tests check that the launches of a plan compute every output cell
+exactly once, for the BASELINE shapes, ragged edges, FFN pairs and several
+CU counts.
+"""
+import ctypes
+import pathlib
+import subprocess
+
+import numpy as np
+import pytest
+
+NATIVE = pathlib.Path(__file__).resolve().parent / "native"
+LIB = NATIVE / "libc4q_probe.so"
+
+TILE_256 = 0
+TILE_128_K128 = 4
+TILE_64x128_K128 = 5
+
+
+@pytest.fixture(scope="module")
+def probe():
+    if not LIB.exists():
+        subprocess.run(["make", "-C", str(NATIVE)], check=True)
+    lib = ctypes.CDLL(str(LIB))
+    f = lib.c4q_probe_tile_plan
+    f.argtypes = [ctypes.c_int64] * 3 + [ctypes.c_int, ctypes.c_void_p, ctypes.c_int64,
+                                         ctypes.c_void_p]
+    f.restype = ctypes.c_int
+    return f
+
+
+def plan(probe, M, n_rows_b, K, cus):
+    cover = np.zeros(-(-M // 64) * -(-n_rows_b // 128), np.int32)
+    info = np.zeros(8, np.int64)
+    assert probe(M, n_rows_b, K, cus, cover.ctypes.data, cover.size, info.ctypes.data) == 0
+    return cover, info
+
+
+# (M, rows of the B tile space, K): BASELINE C1-C5 linears (FLUX QKV / out /
+# MLP up / down, C1 int8, Krea2 pair as 2 * N_out), ragged and tiny shapes
+SHAPES = [
+    (9216, 9216, 3072), (9216, 3072, 3072), (9216, 12288, 3072), (9216, 3072, 12288),
+    (1024, 3072, 3072), (4096, 2 * 12288, 3072), (4352, 4352, 512), (4312, 4280, 512),
+    (4352, 2 * 2176, 512), (9280, 9216, 3072), (300, 1000, 64), (1, 16, 16), (65, 129, 32),
+    (8192, 12288, 3072), (16384, 5120, 5120), (2000, 70000, 128), (5000, 5000, 16),
+]
+
+
+@pytest.mark.parametrize("cus", [256, 304, 80])
+@pytest.mark.parametrize("M,NB,K", SHAPES)
+def test_every_cell_computed_once(probe, M, NB, K, cus):
+    cover, info = plan(probe, M, NB, K, cus)
+    assert info[0] in (1, 2)
+    assert cover.min() == 1 and cover.max() == 1, (
+        f"{M}x{NB}: cells covered {cover.min()}..{cover.max()} (plan {info.tolist()})")
+
+
+def test_random_shapes_computed_once(probe):
+    rng = np.random.default_rng(0)
+    for _ in range(300):
+        M = int(rng.integers(1, 12000))
+        NB = int(rng.integers(1, 12000))
+        K = int(rng.choice([16, 64, 512, 3072, 12288]))
+        cus = int(rng.choice([256, 304, 120, 8]))
+        cover, info = plan(probe, M, NB, K, cus)
+        assert cover.min() == 1 and cover.max() == 1, (M, NB, K, cus, info.tolist())
+
+
+def test_c2_qkv_runs_whole_rounds_then_split_tail(probe):
+    """C2 fused QKV on 256 CUs: 36 x 36 = 1296 tiles of 256x256 are five whole
+    rounds (1280 tiles) plus 16; those 16 run as 128 pieces of 64x128."""
+    _, info = plan(probe, 9216, 9216, 3072, 256)
+    assert info[0] == 2
+    assert (info[1], info[2]) == (TILE_256, 1280)
+    assert (info[3], info[4]) == (TILE_64x128_K128, 16 * 8)
+    assert (info[6], info[7]) == (4, 2)
+
+
+def test_whole_rounds_need_no_tail(probe):
+    """8192 x 12288 is 1536 = 6 x 256 tiles: one launch."""
+    _, info = plan(probe, 8192, 12288, 3072, 256)
+    assert info[0] == 1 and info[1] == TILE_256 and info[2] == 1536
+
+
+def test_ragged_out_proj_keeps_one_launch(probe):
+    """C2 out-proj (432 tiles): a second round of big tiles is cheaper than
+    splitting 176 leftover tiles."""
+    _, info = plan(probe, 9216, 3072, 3072, 256)
+    assert info[0] == 1 and info[1] == TILE_256
+
+
+def test_tail_of_128x128_pieces(probe):
+    """4608 x 4608: 324 tiles, 68 leftover; as 128x128 pieces (272) they fill
+    one round of two workgroups per CU."""
+    _, info = plan(probe, 4608, 4608, 1024, 256)
+    assert info[0] == 2 and (info[1], info[2]) == (TILE_256, 256)
+    assert (info[3], info[4]) == (TILE_128_K128, 68 * 4) and (info[6], info[7]) == (2, 2)
