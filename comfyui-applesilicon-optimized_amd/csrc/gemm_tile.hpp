@@ -87,6 +87,41 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const uint8_t* base,
 }
 constexpr int kOOB = 0x7FFFFFF0;   // an offset past any range
 
+// One buffer_load_dwordx4 ... lds: each lane's 16 bytes at voff + soff of
+// the resource land at lds_addr + 16 * lane. Issued as inline assembly so
+// that the compiler does not track it as an LDS store: tracked, it would
+// wait for every copy in flight (vmcnt(0)) before any later LDS access it
+// cannot prove disjoint -- the fragment reads of other stages and the
+// epilogue strips. The kernels order copies and reads themselves: a stage
+// is read only after each copying wave's vmcnt wait and a barrier, and a
+// buffer is refilled only after a barrier that follows its last reads.
+// m0 (the LDS base of the copy) is set inside the statement; nothing else
+// in these kernels reads m0.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// The words of a raw buffer resource over [base, base + bytes) (as
+// make_rsrc), kept in scalar registers for lds_dma16.
+__device__ __forceinline__ u32x4 dma_rsrc(const uint8_t* base, int64_t bytes) {
+  const uint32_t n = bytes > 0x7FFFFFF0ll ? 0x7FFFFFF0u : (uint32_t)(bytes < 0 ? 0 : bytes);
+  const uint64_t a = (uint64_t)(uintptr_t)base;
+  u32x4 r;
+  r.x = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  r.y = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32) & 0xFFFFu);   // stride 0
+  r.z = __builtin_amdgcn_readfirstlane(n);
+  r.w = 0x00020000u;
+  return r;
+}
+
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_dma16(u32x4 rsrc, const uint8_t* lds, int voff, int soff) {
+  const uint32_t addr = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const uint8_t*)lds);
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :: "s"(addr), "v"(voff), "s"(rsrc), "s"(soff) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
 // Direct global->LDS copy of one stage of a ROWS x ROWB-byte operand slab.
 // One buffer_load_dwordx4 ... lds moves 1 KB: lane L fills LDS row
 // RPI*q + L/CPR at physical chunk L%CPR, so it fetches the logical chunk
@@ -113,33 +148,33 @@ struct DirectLoad {
   int voff[kOff];
   int kofs;                   // byte offset of this lane's chunk within the stage row
   int step;                   // plain operands: bytes between the rows of consecutive copies
-  __device__ __forceinline__ void init(int64_t ld_bytes) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    kofs = ((lane % CPR) ^ Swz<ROWB>::f(RPI * wave + lane / CPR)) * 16;
+  int wv;                     // this wave's index among the NT / 64 copying waves
+  int row0;                   // first stage row the copying waves fill (a multiple of 64)
+  __device__ __forceinline__ void init(int64_t ld_bytes, int wave, int first_row) {
+    const int lane = threadIdx.x & 63;
+    wv = __builtin_amdgcn_readfirstlane(wave);          // wave-uniform: keeps copy
+    row0 = __builtin_amdgcn_readfirstlane(first_row);   // addresses in scalar registers
+    kofs = ((lane % CPR) ^ Swz<ROWB>::f(row0 + RPI * wave + lane / CPR)) * 16;
     step = (int)(RPI * kWaves * ld_bytes);
 #pragma unroll
     for (int j = 0; j < kOff; ++j) {
-      const int q = wave + kWaves * j;
-      const int r = RPI * q + lane / CPR;                      // LDS row
-      const int blk = (RPI * q) >> 5;
-      const int src = PAIR ? ((blk >> 1) * 32 + ((RPI * q) & 31) + lane / CPR) : r;
+      const int rq = row0 + RPI * (wave + kWaves * j);          // first LDS row of copy j
+      const int r = rq + lane / CPR;
+      const int src = PAIR ? ((rq >> 6) * 32 + (rq & 31) + lane / CPR) : r;
       voff[j] = (int)(src * ld_bytes) + kofs;
     }
   }
   // Copy K bytes [kb, kb + ROWB) of every row into `lds`; bytes at or past
   // k_bytes read zeros.
-  __device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t r0, __amdgpu_buffer_rsrc_t r1,
+  __device__ __forceinline__ void issue(u32x4 r0, u32x4 r1,
                                         uint8_t* lds, int kb, int k_bytes) const {
-    const int wave = threadIdx.x >> 6;
     const bool in_k = kb + kofs < k_bytes;
 #pragma unroll
     for (int j = 0; j < kInstr; ++j) {
-      const int q = wave + kWaves * j;
-      const __amdgpu_buffer_rsrc_t rs = (PAIR && (((RPI * q) >> 5) & 1)) ? r1 : r0;
+      const int rq = row0 + RPI * (wv + kWaves * j);
+      const u32x4 rs = (PAIR && ((rq >> 5) & 1)) ? r1 : r0;
       const int vo = PAIR ? voff[PAIR ? j : 0] : voff[0] + j * step;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rs, (__attribute__((address_space(3))) void*)(lds + (RPI * q) * ROWB), 16,
-          in_k ? vo : kOOB, kb, 0, 0);
+      lds_dma16(rs, lds + rq * ROWB, in_k ? vo : kOOB, kb);
     }
   }
 };
@@ -151,6 +186,19 @@ struct DirectLoad {
 // plain decode of an unscaled fp8 weight.
 template <bool BF16, bool HAS_SCALE>
 __device__ __forceinline__ void dequant4(uint32_t w, float s, uint32_t& lo, uint32_t& hi) {
+  if constexpr (!HAS_SCALE) {
+    // e4m3fn -> bf16/f16 is exact; the scaled conversion with scale 1.0 (a
+    // power of two, the only scales it applies exactly) does two codes per
+    // instruction
+    if constexpr (BF16) {
+      lo = bitcast<uint32_t>(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false));
+      hi = bitcast<uint32_t>(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true));
+    } else {
+      lo = bitcast<uint32_t>(__builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, false));
+      hi = bitcast<uint32_t>(__builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, true));
+    }
+    return;
+  }
   f32x2 a = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
   f32x2 b = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
   if (HAS_SCALE) { a.x *= s; a.y *= s; b.x *= s; b.y *= s; }
@@ -184,6 +232,7 @@ template <int KS>
 struct OpI8T {
   using Acc = i32x16;
   static constexpr int kStageK = KS, SA = KS, SB = KS, S = KS / 32;
+  static constexpr bool kPingPong = false;   // see gemm_pingpong_kernel
   template <int TM, int TN> struct Frag { i32x4 a[TM], b[TN]; };
   __device__ __forceinline__ static float prep_scale(const float*) { return 1.0f; }
   template <int TM, int TN>
@@ -212,6 +261,7 @@ template <int KS>
 struct OpF8T {
   using Acc = f32x16;
   static constexpr int kStageK = KS, SA = KS, SB = KS, S = KS / 64;
+  static constexpr bool kPingPong = false;
   template <int TM, int TN> struct Frag { i32x8 a[TM], b[TN]; };
   __device__ __forceinline__ static float prep_scale(const float*) { return 1.0f; }
   template <int ROWB>
@@ -257,6 +307,7 @@ template <bool BF16, bool HAS_SCALE>
 struct OpW8A16 {
   using Acc = f32x16;
   static constexpr int kStageK = 64, SA = 128, SB = 64, S = 2;
+  static constexpr bool kPingPong = true;
   template <int TM, int TN> struct Frag { i32x4 a[2][TM], q[TN]; };
   // per-tensor weight scale rounded to the activation type (scale.to(T))
   __device__ __forceinline__ static float prep_scale(const float* sp) {
@@ -608,23 +659,23 @@ gemm_tile_kernel(GemmShape sh, Src2 sa, Src2 sb, const float* b_scale, Epi epi) 
 
   LA la;
   LB lb;
-  la.init(sa.ld_bytes);
-  lb.init(sb.ld_bytes);
+  la.init(sa.ld_bytes, wave, 0);
+  lb.init(sb.ld_bytes, wave, 0);
   constexpr int KS = Op::kStageK;
   const int a_kb = (int)(sh.K * SA / KS), b_kb = (int)(sh.K * SB / KS);
   const int nst = (int)((sh.K + KS - 1) / KS);
 
   // Copy cursor: next stage to issue is stage ips of this workgroup's tile ij.
   int ij = 0, ips = 0;
-  __amdgpu_buffer_rsrc_t ra, rb0, rb1;
+  u32x4 ra, rb0, rb1;
   auto tile_rsrc = [&](int j) {
     const TileCoord tc = tile_at(sh, (int)blockIdx.x + j * G);
     const int64_t m0 = (int64_t)tc.tm * BM;
     const int64_t brow0 = PAIR ? ((int64_t)tc.tn * BN >> 1) : (int64_t)tc.tn * BN;
     const int64_t bleft = (sb.rows - brow0) * sb.ld_bytes;
-    ra = make_rsrc(sa.p0 + m0 * sa.ld_bytes, (sa.rows - m0) * sa.ld_bytes);
-    rb0 = make_rsrc(sb.p0 + brow0 * sb.ld_bytes, bleft);
-    rb1 = PAIR ? make_rsrc(sb.p1 + brow0 * sb.ld_bytes, bleft) : rb0;
+    ra = dma_rsrc(sa.p0 + m0 * sa.ld_bytes, (sa.rows - m0) * sa.ld_bytes);
+    rb0 = dma_rsrc(sb.p0 + brow0 * sb.ld_bytes, bleft);
+    rb1 = PAIR ? dma_rsrc(sb.p1 + brow0 * sb.ld_bytes, bleft) : rb0;
   };
   // Issue the next stage into `buf`; past this workgroup's last tile the
   // copies read zeros (every stage issues the same number of copies, which
@@ -701,6 +752,139 @@ gemm_tile_kernel(GemmShape sh, Src2 sa, Src2 sb, const float* b_scale, Epi epi) 
       epilogue_single<TM, TN>(acc, wm0, (int64_t)tc.tn * BN + wn * (TN * 32), sh.M, sh.N, ep, strip);
     }
   }
+  wait_vm<0>();    // zero-fill copies past the last tile still target the ring
+}
+
+// Ping-pong schedule of the 8-wave tile (WM = 2, WN = 4). The two wave
+// rows are two groups (waves 0-3 and 4-7, one of each on every SIMD) that
+// own the upper and lower halves of the tile and run half a stage apart:
+//
+//   group 0:  | mem k   | mma k   | mem k+1 | mma k+1 | ...
+//   group 1:  |         | mem k   | mma k   | mem k+1 | ...
+//                       ^ one workgroup barrier between intervals
+//
+// In its memory interval a group reads all fragments of stage k from LDS
+// and issues its half of the copies of stage k + NBUF - 1 (its A rows, half
+// of the B rows) into the buffer both groups finished reading one interval
+// earlier; in its MFMA interval it multiplies from registers only. Each
+// SIMD's MFMA pipe is fed by one group while the other group's LDS reads,
+// copies and address work proceed, instead of both waves of a SIMD wanting
+// the MFMA pipe and the LDS at the same moments. A tile's epilogue runs in
+// its group's next memory interval. Stage k (both halves) is complete before
+// barrier 2k, where group 0 starts reading it: group 0 waits for its copies
+// at the end of its MFMA interval, group 1 at the end of its memory
+// interval, in both cases for the copies it issued NBUF - 2 stages earlier.
+template <class Op, int BM, int BN, int NBUF, bool PAIR, class Epi>
+__global__ void __launch_bounds__(512)
+gemm_pingpong_kernel(GemmShape sh, Src2 sa, Src2 sb, const float* b_scale, Epi epi) {
+  constexpr int WM = 2, WN = 4, NT = 512;
+  constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
+  static_assert(TM >= 1 && TN >= 1 && TM * WM * 32 == BM && TN * WN * 32 == BN, "bad wave tiling");
+  static_assert(!PAIR || (TN % 2 == 0), "pair tiles need whole gate/up block pairs");
+  static_assert((BM / 2) % 64 == 0 && (BN / 2) % 64 == 0, "group halves must align to 64 rows");
+  constexpr int SA = Op::SA, SB = Op::SB, S = Op::S;
+  constexpr int STAGE = BM * SA + BN * SB;
+  constexpr int RING = NBUF * STAGE;
+  constexpr int kStrip = strip_bytes<TN, PAIR>();
+  static_assert(NBUF >= 3 && RING + kStrip * WM * WN <= 160 * 1024, "LDS exceeds 160 KB");
+  using LA = DirectLoad<BM / 2, SA, NT / 2, false>;
+  using LB = DirectLoad<BN / 2, SB, NT / 2, PAIR>;
+  constexpr int kPerStage = LA::kInstr + LB::kInstr;     // copies per wave per stage
+  static_assert((NBUF - 1) * kPerStage < 64, "too many copies in flight for vmcnt");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[RING + kStrip * WM * WN];
+
+  const int ntiles = sh.count;
+  const int G = (int)gridDim.x;
+  const int my_tiles = (ntiles - 1 - (int)blockIdx.x) / G + 1;
+  const Epi ep = epi.prepare();
+  const int wave = threadIdx.x >> 6;
+  const int grp = __builtin_amdgcn_readfirstlane(wave >> 2), wn = wave & 3;
+  const float ws = Op::prep_scale(b_scale);
+
+  LA la;
+  LB lb;
+  la.init(sa.ld_bytes, wn, grp * (BM / 2));
+  lb.init(sb.ld_bytes, wn, grp * (BN / 2));
+  constexpr int KS = Op::kStageK;
+  const int a_kb = (int)(sh.K * SA / KS), b_kb = (int)(sh.K * SB / KS);
+  const int nst = (int)((sh.K + KS - 1) / KS);
+
+  int ij = 0, ips = 0;
+  u32x4 ra, rb0, rb1;
+  auto tile_rsrc = [&](int j) {
+    const TileCoord tc = tile_at(sh, (int)blockIdx.x + j * G);
+    const int64_t m0 = (int64_t)tc.tm * BM;
+    const int64_t brow0 = PAIR ? ((int64_t)tc.tn * BN >> 1) : (int64_t)tc.tn * BN;
+    const int64_t bleft = (sb.rows - brow0) * sb.ld_bytes;
+    ra = dma_rsrc(sa.p0 + m0 * sa.ld_bytes, (sa.rows - m0) * sa.ld_bytes);
+    rb0 = dma_rsrc(sb.p0 + brow0 * sb.ld_bytes, bleft);
+    rb1 = PAIR ? dma_rsrc(sb.p1 + brow0 * sb.ld_bytes, bleft) : rb0;
+  };
+  auto issue_next = [&](uint8_t* buf) {
+    if (ij < my_tiles) {
+      la.issue(ra, ra, buf, ips * SA, a_kb);
+      lb.issue(rb0, rb1, buf + BM * SA, ips * SB, b_kb);
+      if (++ips == nst) {
+        ips = 0;
+        if (++ij < my_tiles) tile_rsrc(ij);
+      }
+    } else {
+      la.issue(ra, ra, buf, 0, 0);
+      lb.issue(rb0, rb1, buf + BM * SA, 0, 0);
+    }
+  };
+  tile_rsrc(0);
+
+  // prologue: stages 0 .. NBUF-2 in flight; stage 0 complete and visible
+#pragma unroll
+  for (int p = 0; p < NBUF - 1; ++p) issue_next(smem + p * STAGE);
+  wait_vm<(NBUF - 2) * kPerStage>();
+  stage_barrier();
+  if (grp == 1) stage_barrier();               // group 1 runs one interval behind
+
+  const int ra0 = grp * (TM * 32), rb0i = wn * (TN * 32);
+  using Frag = typename Op::template Frag<TM, TN>;
+  Frag fr[S];
+  uint8_t* strip = smem + RING + wave * kStrip;
+  typename Op::Acc acc[TM][TN];
+  int gs = 0;                                   // stage counter over all tiles
+  for (int j = 0; j < my_tiles; ++j) {
+    for (int st = 0; st < nst; ++st, ++gs) {
+      // memory interval
+      const uint8_t* cur = smem + (gs % NBUF) * STAGE;
+#pragma unroll
+      for (int s = 0; s < S; ++s) Op::template frags<TM, TN>(fr[s], cur, cur + BM * SA, ra0, rb0i, s);
+      issue_next(smem + ((gs + NBUF - 1) % NBUF) * STAGE);
+      if (grp == 1) wait_vm<(NBUF - 2) * kPerStage>();
+      __builtin_amdgcn_sched_barrier(0);
+      stage_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      // MFMA interval
+      if (st == 0) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int jj = 0; jj < TN; ++jj)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][jj][r] = 0;
+      }
+#pragma unroll
+      for (int s = 0; s < S; ++s) Op::template mma<TM, TN>(fr[s], acc, ws);
+      if (grp == 0) wait_vm<(NBUF - 2) * kPerStage>();
+      __builtin_amdgcn_sched_barrier(0);
+      stage_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    const TileCoord tc = tile_at(sh, (int)blockIdx.x + j * G);
+    const int64_t wm0 = (int64_t)tc.tm * BM + grp * (TM * 32);
+    if constexpr (PAIR) {
+      const int64_t c0 = ((int64_t)tc.tn * BN >> 1) + wn * (TN * 16);
+      epilogue_pair<TM, TN>(acc, wm0, c0, sh.M, sh.N >> 1, ep, strip);
+    } else {
+      epilogue_single<TM, TN>(acc, wm0, (int64_t)tc.tn * BN + wn * (TN * 32), sh.M, sh.N, ep, strip);
+    }
+  }
+  if (grp == 0) stage_barrier();               // matches group 1's extra barrier
   wait_vm<0>();    // zero-fill copies past the last tile still target the ring
 }
 

@@ -72,9 +72,41 @@ int persistent_grid(K kernel, int nt, int64_t tiles, int& occ) {
   return (int)(tiles < slots ? tiles : slots);
 }
 
+// Operand policy of the ping-pong kernel: 8-bit operands stage 64 K, so
+// that the ring holds four stages (copies run three stages ahead).
+template <class Op> struct PingPongOp { using type = Op; };
+template <> struct PingPongOp<OpI8T<128>> { using type = OpI8T<64>; };
+template <> struct PingPongOp<OpF8T<128>> { using type = OpF8T<64>; };
+
+// The 8-wave tiles take the ping-pong schedule where the operand policy asks
+// for it (W8A16: its 48 KB stage leaves a three-stage ring, and the dequant
+// work lengthens the MFMA interval against the memory interval; MI355X,
+// FLUX shapes: +1-3%). 8-bit operands keep the one-group schedule, whose
+// 128-K stages beat the 64-K stages ping-pong needs (-5-10% with them).
+// C4Q_PINGPONG=0 / 1 in the environment forces either, for tuning sweeps.
+template <class Op>
+inline bool pingpong_on() {
+  const char* e = getenv("C4Q_PINGPONG");
+  if (e && (e[0] == '0' || e[0] == '1') && e[1] == 0) return e[0] == '1';
+  return Op::kPingPong;
+}
+
 template <class T, class Op, bool PAIR, class Epi>
 int launch_tile(const GemmShape& sh, const Src2& sa, const Src2& sb, const float* b_scale,
                 const Epi& epi, hipStream_t s, const char* what) {
+  if constexpr (T::WM == 2 && T::WN == 4) {
+    using POp = typename PingPongOp<Op>::type;
+    constexpr int pbuf = ring_depth<T, POp, PAIR>();
+    if constexpr (pbuf >= 3) {
+      if (pingpong_on<Op>()) {
+        auto kernel = gemm_pingpong_kernel<POp, T::BM, T::BN, pbuf, PAIR, Epi>;
+        static int pocc = 0;
+        const int grid = persistent_grid(kernel, T::NT, sh.count, pocc);
+        hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(T::NT), 0, s, sh, sa, sb, b_scale, epi);
+        return check_launch(what);
+      }
+    }
+  }
   constexpr int nbuf = ring_depth<T, Op, PAIR>();
   auto kernel = gemm_tile_kernel<Op, T::BM, T::BN, T::WM, T::WN, nbuf, PAIR, Epi>;
   static int occ = 0;

@@ -280,6 +280,30 @@ def test_w8a16_linear(dev, M, K, N, xdt, scaled, bias_dt):
     assert_close(tof(bits16(out)), tof(ref), f"w8a16 {M}x{K}x{N}")
 
 
+@pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("scale", [None, 0.0123, 2.0 ** -7, 3.7])
+@pytest.mark.parametrize("M", [256, 8])
+def test_w8a16_dequant_exact_every_code(dev, xdt, scale, M):
+    """The in-register weight dequant, bit for bit: with an identity
+    activation each output y[i, n] is the single product 1 * W'[n, i], exact
+    in fp32 and in the output type, so y is the dequantized weight
+    T(decode(w) * T(scale)) (comfykitchen_fp8.py:86-89) of every finite
+    e4m3fn code. M = 256 takes the MFMA-tiled route, M = 8 the small-M one."""
+    K = N = 256
+    codes = (np.arange(N)[:, None] + np.arange(K)[None, :]) % 256
+    codes[(codes & 0x7F) == 0x7F] = 0                     # the two NaN codes
+    w = torch.from_numpy(codes.astype(np.uint8)).view(torch.float8_e4m3fn)
+    x = torch.zeros(M, K, dtype=xdt)
+    x[torch.arange(M), torch.arange(M)] = 1
+    ws = None if scale is None else torch.tensor([scale], dtype=torch.float32)
+    y = ops.w8a16_linear(x.to(dev), w.to(dev), None if ws is None else ws.to(dev))
+    od = "bf16" if xdt == torch.bfloat16 else "f16"
+    deq = of.dequant_pertensor(codes.astype(np.uint8), None if ws is None else ws.numpy(), od)
+    want = np.ascontiguousarray(deq.T[:M])
+    want[want == 0x8000] = 0      # -0 (code 0x80) plus the +0 products of the sum is +0
+    assert_bits_equal(bits16(y), want, f"dequant {od} scale={scale} M={M}")
+
+
 @pytest.mark.parametrize("M,K,N,xdt,scaled,bias_dt,out_dt", [
     (1, 3072, 3072, torch.bfloat16, True, torch.bfloat16, None),     # decode shapes (16 waves)
     (4, 3072, 8200, torch.bfloat16, True, torch.bfloat16, None),     # 8-wave split, ragged N
