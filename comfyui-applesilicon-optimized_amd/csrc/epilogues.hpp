@@ -62,6 +62,12 @@ __device__ __forceinline__ float load_f32(const void* p, int dt, int64_t i) {
   if (dt == DT_F16) return f16_f32(static_cast<const uint16_t*>(p)[i]);
   return static_cast<const float*>(p)[i];
 }
+// f32 value of raw bias bits (f32, or bf16/f16 in the low half).
+__device__ __forceinline__ float raw_f32(uint32_t raw, int dt) {
+  if (dt == DT_BF16) return bf16_f32((uint16_t)raw);
+  if (dt == DT_F16) return f16_f32((uint16_t)raw);
+  return __builtin_bit_cast(float, raw);
+}
 
 template <class T>
 struct EpiOut {

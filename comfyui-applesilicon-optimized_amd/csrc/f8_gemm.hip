@@ -60,25 +60,44 @@ int run_w8a16_skinny(const uint16_t* a, int64_t lda, const uint8_t* w, int64_t l
                      hipStream_t s, const char* what) {
   const int64_t nblk = cdiv(N, 16);
   const int64_t nch = cdiv(K, 64);
-  auto launch = [&](auto kernel, int cpw, int maxw, int& occ) {
+  auto launch = [&](auto kernel, int cpw, int& occ) {
     const int waves = (int)cdiv(nch, cpw);
     if (occ <= 0) {
       int o = 0;
-      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, kernel, 64 * maxw, 0) != hipSuccess || o < 1)
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, kernel, 64 * waves, 0) != hipSuccess || o < 1)
         o = 1;
       occ = o;
     }
-    // occupancy was taken at the largest block size; smaller blocks fit at
-    // least as many workgroups per CU
-    const int64_t slots = (int64_t)device_cus() * occ * (maxw / waves);
+    const int64_t slots = (int64_t)device_cus() * occ;
     const int64_t rounds = cdiv(nblk, slots);
     const int64_t grid = cdiv(nblk, rounds);
     hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(64 * waves), 0, s, a, lda, w, ldw, w_scale,
                        M, N, K, epi);
     return check_launch(what);
   };
-  static int occ4 = 0;
-  return launch(w8a16_skinny_kernel<BF16, HAS_SCALE, 4, kSkinnyMaxWaves, Epi>, 4, kSkinnyMaxWaves, occ4);
+  // K <= 3072: at most 12 waves of 4 chunks, 6 blocks per barrier; up to
+  // 4096: 16 waves, 4 blocks per barrier (the partial-tile area keeps one
+  // workgroup per CU either way). Weight blocks in flight per wave: 2 for
+  // M <= 4 with two or more blocks per workgroup, else 1 (the loads of one
+  // block per wave across 12 waves already cover the HBM latency; deeper
+  // prefetch only pays where each block's arithmetic is short -- MI355X,
+  // N = 18432 / 3072, K = 3072). The bias width is a template parameter.
+  const int64_t slots = (int64_t)device_cus();
+  const bool deep = M <= 4 && cdiv(nblk, slots) >= 2;
+  auto pick = [&](auto bias_bits, auto depth) {
+    constexpr int BIAS = decltype(bias_bits)::value, D = decltype(depth)::value;
+    static int occ12 = 0, occ16 = 0;
+    if (nch <= 4 * 12)
+      return launch(w8a16_skinny_kernel<BF16, HAS_SCALE, 4, 12, D, 6, BIAS, Epi>, 4, occ12);
+    return launch(w8a16_skinny_kernel<BF16, HAS_SCALE, 4, kSkinnyMaxWaves, D, 4, BIAS, Epi>, 4, occ16);
+  };
+  auto with_depth = [&](auto bias_bits) {
+    return deep ? pick(bias_bits, std::integral_constant<int, 2>{})
+                : pick(bias_bits, std::integral_constant<int, 1>{});
+  };
+  if (!epi.bias) return with_depth(std::integral_constant<int, 0>{});
+  if (epi.bias_dt == DT_F32) return with_depth(std::integral_constant<int, 32>{});
+  return with_depth(std::integral_constant<int, 16>{});
 }
 
 template <class Epi>
@@ -88,7 +107,10 @@ int run_w8a16(const void* a, int a_dtype, int64_t lda, const uint8_t* w, int64_t
   const bool bf16 = a_dtype == C4Q_BF16;
   // The skinny kernel addresses a 16-row weight block and the activation
   // rows with 32-bit buffer offsets.
+  // (the small-M kernel reads the bias through the scalar cache: a 4-byte
+  // aligned base)
   const bool skinny = M <= kSkinnyMaxM && K > 0 && K <= kSkinnyMaxK && aligned16(a) &&
+                      (epi.bias == nullptr || ((uintptr_t)epi.bias & 3) == 0) &&
                       aligned16(w) && lda % 8 == 0 && ldw % 16 == 0 && 16 * ldw + 64 < (1ll << 31) &&
                       kSkinnyMaxM * 2 * lda + 256 < (1ll << 31);
   if (skinny) {

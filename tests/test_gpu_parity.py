@@ -316,6 +316,9 @@ def test_w8a16_dequant_exact_every_code(dev, xdt, scale, M):
     (2, 4096, 96, torch.bfloat16, True, torch.bfloat16, None),       # largest K of the small-M route
     (2, 4112, 96, torch.bfloat16, True, torch.bfloat16, None),       # K past it: tiled route
     (16, 3072, 18432, torch.bfloat16, True, torch.bfloat16, None),   # several blocks per workgroup
+    (2, 512, 100000, torch.bfloat16, True, torch.bfloat16, None),    # several reduction groups
+    (16, 4096, 20000, torch.bfloat16, True, torch.float32, None),    # 16-wave variant, two groups
+    (9, 3000, 33333, torch.float16, False, torch.bfloat16, None),    # ragged K and N, last group short
 ])
 def test_w8a16_small_m(dev, M, K, N, xdt, scaled, bias_dt, out_dt):
     """Small-M (split-K) route against the oracle's dequant + fp32-accumulated
