@@ -7,8 +7,9 @@ Prints ONE JSON line. The headline (``value``) is BASELINE config C2: the
 FLUX-style DiT W8A16 step, i.e. the fused-QKV (3072->9216) and out-proj
 (3072->3072) fp8-e4m3fn-weight linears over X [2*4608, 3072] bf16, in
 TFLOP/s (2*M*K*N per linear). ``roofline`` covers the dominant kernel of
-that step (the QKV W8A16 GEMM), timed with HIP events around each of its
-launches inside the timed region. ``per_config`` adds C1, C3, C4 and C5
+that step (the QKV W8A16 GEMM: one launch of whole rounds of 256x256 tiles
+plus one launch of the leftover tiles as split-K 64x64 pieces), timed with HIP
+events around each QKV call inside the timed region. ``per_config`` adds C1, C3, C4 and C5
 measured in the same process; ``cpu_baseline`` times the reference's
 PyTorch CPU path for C2 (kitchen dequant + bf16 F.linear) on a bounded row
 sample on this host's cores.
@@ -120,7 +121,8 @@ def bench_c2(torch, ops, dev, steps, warmup):
     qkv_flops = 2.0 * M * K * Ns[0]
     return {
         "flops": flops, "wall_s": wall, "tflops": flops / wall / 1e12,
-        "kernel": "W8A16 GEMM (256x256 tile) fused-QKV 9216x3072 -> 9216",
+        "kernel": ("W8A16 GEMM fused-QKV 9216x3072 -> 9216: 1280 tiles of 256x256 "
+                   "(ping-pong schedule) + 16 leftover tiles as 256 split-K pieces of 64x64"),
         "kernel_s": kern, "kernel_flops": qkv_flops,
         "kernel_tflops": qkv_flops / kern / 1e12 if kern else None,
     }
@@ -314,6 +316,8 @@ def bench_c5(torch, ops, dev, steps, warmup):
 # ------------------------------------------------------------- traffic ---
 # HBM traffic of the headline kernel from two rocprofv3 counter passes over
 # `bench.py --pmc-target` (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch).
+# One QKV call is PMC_CALLS-th of the W8A16 dispatches (main + tail launch);
+# its traffic is the sum over its dispatches.
 # The same run first copies COPY_BYTES with a plain device copy; the factor
 # algorithmic bytes / counted bytes of that copy calibrates each counter.
 # `bench.py --pmc-summarize FETCH_DIR WRITE_DIR` writes TRAFFIC_FILE, which
@@ -321,6 +325,7 @@ def bench_c5(torch, ops, dev, steps, warmup):
 COPY_BYTES = 512 * 1024 * 1024
 TRAFFIC_FILE = ROOT / "profiles" / "w8a16_gemm_c2_qkv_traffic.json"
 QKV_KERNEL_KEY = "OpW8A16"
+PMC_CALLS = 3
 
 
 def pmc_target(torch, ops, dev):
@@ -332,7 +337,7 @@ def pmc_target(torch, ops, dev):
     del src, dst
     x, layers = make_c2(torch, dev)
     q, s, b = layers[0]
-    for _ in range(3):
+    for _ in range(PMC_CALLS):
         ops.w8a16_linear(x, q, s, b)
     torch.cuda.synchronize()
 
@@ -353,19 +358,22 @@ def pmc_summarize(fetch_dir, write_dir):
     for counter, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
         rows = _pmc_rows(d, counter)
         copies = [v for _, k, v in rows if "copyBuffer" in k]      # dst.copy_(src): the runtime's blit
-        qkv = [v for _, k, v in rows if "gemm_tile_kernel" in k and QKV_KERNEL_KEY in k]
-        if not copies or not qkv:
+        qkv = [(k, v) for _, k, v in rows if "c4q::gemm_" in k and QKV_KERNEL_KEY in k]
+        if not copies or not qkv or len(qkv) % PMC_CALLS:
             raise SystemExit(f"{counter}: copy or QKV dispatches not found in {d}")
+        per_call = len(qkv) // PMC_CALLS
         copy_kib = statistics.median(copies[-3:])
         factor = (COPY_BYTES / 1024.0) / copy_kib
-        kib = statistics.median(qkv)
+        calls = [qkv[i:i + per_call] for i in range(0, len(qkv), per_call)]
+        kib = statistics.median(sum(v for _, v in c) for c in calls)
         out[counter] = {"copy_kib_per_dispatch": copy_kib, "factor": factor,
-                        "qkv_kib_per_dispatch": kib, "qkv_bytes": kib * 1024.0 * factor}
+                        "qkv_kib_per_call": kib, "qkv_bytes": kib * 1024.0 * factor,
+                        "dispatches_per_call": [[k.split("(")[0], v] for k, v in calls[0]]}
     M, K, N = 9216, 3072, 9216
     algo = M * K * 2 + N * K + N * 2 + 4 + M * N * 2   # X bf16 + W fp8 + bias bf16 + scale + Y bf16
     out["traffic_bytes"] = out["FETCH_SIZE"]["qkv_bytes"] + out["WRITE_SIZE"]["qkv_bytes"]
     out["algorithmic_bytes"] = algo
-    out["kernel"] = "W8A16 GEMM fused-QKV 9216x3072 -> 9216 (C2)"
+    out["kernel"] = "W8A16 GEMM fused-QKV 9216x3072 -> 9216 (C2), main + tail launch"
     TRAFFIC_FILE.write_text(json.dumps(out, indent=1) + "\n")
     print(json.dumps(out))
 

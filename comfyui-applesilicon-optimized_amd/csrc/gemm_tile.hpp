@@ -888,4 +888,146 @@ gemm_pingpong_kernel(GemmShape sh, Src2 sa, Src2 sb, const float* b_scale, Epi e
   wait_vm<0>();    // zero-fill copies past the last tile still target the ring
 }
 
+// Split-K tile kernel for small pieces (the leftover tiles of a large GEMM,
+// split): KG groups of WM x WN waves share one BM x BN tile. Stage s holds
+// KG consecutive K blocks of kStageK; group g copies and multiplies block
+// s * KG + g into its own slice of the stage, so every group runs the
+// pipeline of gemm_tile_kernel over a quarter (KG = 4) of K, in lockstep
+// with the others at the stage barriers. A wave holds at least a 32 x 64
+// sub-tile; a one-wave-per-SIMD piece of that size is bound by the latency
+// of its own LDS -> dequant -> MFMA chain, and the groups give every SIMD
+// KG / 4 * WM * WN independent chains instead. At the end groups 1..KG-1
+// leave their accumulators in the (drained) ring and group 0 adds them in
+// group order, then runs the epilogue. Pieces are few (at most a round), so
+// each workgroup drains its ring after every piece instead of prefetching
+// the next one.
+template <class Op, int BM, int BN, int WM, int WN, int KG, int NBUF, bool PAIR, class Epi>
+__global__ void __launch_bounds__(64 * WM * WN * KG)
+gemm_splitk_kernel(GemmShape sh, Src2 sa, Src2 sb, const float* b_scale, Epi epi) {
+  constexpr int GW = WM * WN;                            // waves per group
+  constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
+  static_assert(TM >= 1 && TN >= 1 && TM * WM * 32 == BM && TN * WN * 32 == BN, "bad wave tiling");
+  static_assert(!PAIR || (TN % 2 == 0), "pair tiles need whole gate/up block pairs");
+  constexpr int SA = Op::SA, SB = Op::SB, S = Op::S;
+  static_assert(S % 2 == 0, "the fragment double buffer assumes an even step count per stage");
+  constexpr int SUB = BM * SA + BN * SB;                 // one group's K block
+  constexpr int STAGE = KG * SUB;
+  constexpr int RING = NBUF * STAGE;
+  constexpr int kStrip = strip_bytes<TN, PAIR>();
+  using Scalar = std::remove_cv_t<std::remove_reference_t<decltype(typename Op::Acc{}[0])>>;
+  constexpr int kPart = (KG - 1) * GW * TM * TN * 16 * 64 * (int)sizeof(Scalar);
+  static_assert(KG >= 2 && kPart <= RING, "partial sums must fit the ring");
+  static_assert(NBUF >= 2 && RING + kStrip * GW <= 160 * 1024, "LDS exceeds 160 KB");
+  using LA = DirectLoad<BM, SA, 64 * GW, false>;
+  using LB = DirectLoad<BN, SB, 64 * GW, PAIR>;
+  constexpr int kPerStage = LA::kInstr + LB::kInstr;     // copies per wave per stage
+  static_assert((NBUF - 1) * kPerStage < 64, "too many copies in flight for vmcnt");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[RING + kStrip * GW];
+
+  const Epi ep = epi.prepare();
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int grp = wave / GW, gw = wave % GW;
+  const int wm = gw / WN, wn = gw % WN;
+  const int lane = threadIdx.x & 63;
+  const float ws = Op::prep_scale(b_scale);
+
+  LA la;
+  LB lb;
+  la.init(sa.ld_bytes, gw, 0);
+  lb.init(sb.ld_bytes, gw, 0);
+  constexpr int KS = Op::kStageK;
+  const int a_kb = (int)(sh.K * SA / KS), b_kb = (int)(sh.K * SB / KS);
+  const int nblk = (int)((sh.K + KS - 1) / KS);
+  const int nst = (nblk + KG - 1) / KG;                  // stages; blocks past K read zeros
+  const int ra0 = wm * (TM * 32), rb0i = wn * (TN * 32);
+  using Frag = typename Op::template Frag<TM, TN>;
+  Scalar* part = reinterpret_cast<Scalar*>(smem);
+  uint8_t* strip = smem + RING + gw * kStrip;
+
+  for (int t = (int)blockIdx.x; t < sh.count; t += (int)gridDim.x) {
+    const TileCoord tc = tile_at(sh, t);
+    const int64_t m0 = (int64_t)tc.tm * BM;
+    const int64_t brow0 = PAIR ? ((int64_t)tc.tn * BN >> 1) : (int64_t)tc.tn * BN;
+    const int64_t bleft = (sb.rows - brow0) * sb.ld_bytes;
+    const u32x4 ra = dma_rsrc(sa.p0 + m0 * sa.ld_bytes, (sa.rows - m0) * sa.ld_bytes);
+    const u32x4 rb0 = dma_rsrc(sb.p0 + brow0 * sb.ld_bytes, bleft);
+    const u32x4 rb1 = PAIR ? dma_rsrc(sb.p1 + brow0 * sb.ld_bytes, bleft) : rb0;
+    // stage s of this group: K block s * KG + grp (zeros past K, so every
+    // stage issues the same copies and the vmcnt arithmetic stays fixed)
+    auto issue = [&](int s) {
+      uint8_t* buf = smem + (s % NBUF) * STAGE + grp * SUB;
+      const int blk = s * KG + grp;
+      la.issue(ra, ra, buf, blk * SA, a_kb);
+      lb.issue(rb0, rb1, buf + BM * SA, blk * SB, b_kb);
+    };
+#pragma unroll
+    for (int p = 0; p < NBUF; ++p) issue(p);
+    wait_vm<(NBUF - 1) * kPerStage>();
+    stage_barrier();
+
+    typename Op::Acc acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int jj = 0; jj < TN; ++jj)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][jj][r] = 0;
+    Frag fr[2];
+    {
+      const uint8_t* cur = smem + grp * SUB;
+      Op::template frags<TM, TN>(fr[0], cur, cur + BM * SA, ra0, rb0i, 0);
+    }
+    for (int st = 0; st < nst; ++st) {
+      const uint8_t* cur = smem + (st % NBUF) * STAGE + grp * SUB;
+      const uint8_t* nxt = smem + ((st + 1) % NBUF) * STAGE + grp * SUB;
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        if (s == S - 1) {
+          wait_vm<(NBUF - 2) * kPerStage>();   // this wave's copies of stage st+1 landed
+          stage_barrier();                     // ... and every wave's; stage st fully read
+          issue(st + NBUF);                    // refill with stage st+NBUF
+          if (st + 1 < nst) Op::template frags<TM, TN>(fr[0], nxt, nxt + BM * SA, ra0, rb0i, 0);
+        } else {
+          Op::template frags<TM, TN>(fr[(s + 1) & 1], cur, cur + BM * SA, ra0, rb0i, s + 1);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        Op::template mma<TM, TN>(fr[s & 1], acc, ws);
+      }
+    }
+    // every copy (the zero stages past K included) has landed and every
+    // fragment read is done: the ring is free for the partial sums
+    wait_vm<0>();
+    stage_barrier();
+    auto slot = [&](int g, int i, int jj, int r) {
+      return ((((g - 1) * GW + gw) * TM + i) * TN * 16 + jj * 16 + r) * 64 + lane;
+    };
+    if (grp > 0) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int jj = 0; jj < TN; ++jj)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) part[slot(grp, i, jj, r)] = acc[i][jj][r];
+    }
+    stage_barrier();
+    if (grp == 0) {
+      for (int g = 1; g < KG; ++g)
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int jj = 0; jj < TN; ++jj)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][jj][r] += part[slot(g, i, jj, r)];
+      const int64_t wm0 = m0 + wm * (TM * 32);
+      if constexpr (PAIR) {
+        const int64_t c0 = brow0 + wn * (TN * 16);
+        epilogue_pair<TM, TN>(acc, wm0, c0, sh.M, sh.N >> 1, ep, strip);
+      } else {
+        epilogue_single<TM, TN>(acc, wm0, brow0 + wn * (TN * 32), sh.M, sh.N, ep, strip);
+      }
+    }
+    stage_barrier();                           // partial sums read before the ring refills
+  }
+}
+
 }  // namespace c4q

@@ -11,11 +11,13 @@ namespace c4q {
 
 // Tile variants of the MFMA kernels: BM x BN output tile, WM x WN waves,
 // the LDS budget of one workgroup (160 KB: one workgroup per CU; less
-// leaves room for two or three) and the stage depth in K of the 8-bit
-// operand policies (64 or 128).
-template <int BM_, int BN_, int WM_, int WN_, int LDS_KB_, int KS8_>
+// leaves room for two or three), the stage depth in K of the 8-bit operand
+// policies (64 or 128) and the number of K groups (KG > 1: the split-K
+// kernel, KG groups of WM x WN waves).
+template <int BM_, int BN_, int WM_, int WN_, int LDS_KB_, int KS8_, int KG_ = 1>
 struct Tile {
-  static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, NT = 64 * WM_ * WN_;
+  static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, KG = KG_;
+  static constexpr int NT = 64 * WM_ * WN_ * KG_;
   static constexpr int LDS = LDS_KB_ * 1024;
   static constexpr int KS8 = KS8_;
 };
@@ -24,7 +26,7 @@ struct Tile {
 // strips, at most 4.
 template <class T, class Op, bool PAIR>
 constexpr int ring_depth() {
-  constexpr int stage = T::BM * Op::SA + T::BN * Op::SB;
+  constexpr int stage = T::KG * (T::BM * Op::SA + T::BN * Op::SB);
   constexpr int strips = (T::WM * T::WN) * strip_bytes<T::BN / T::WN / 32, PAIR>();
   constexpr int n = (T::LDS - strips) / stage;
   return n > 4 ? 4 : (n < 2 ? 2 : n);
@@ -37,7 +39,8 @@ enum TileId : int {
   TILE_128x128_W4_K128 = 4,
   TILE_64x128_W4_K128 = 5,
   TILE_256x256_W8_K64 = 6,
-  TILE_COUNT = 7,
+  TILE_64x64_KG4 = 7,    // split-K: 4 groups of 2 waves, 32x64 per wave
+  TILE_COUNT = 8,
 };
 
 template <class F>
@@ -49,6 +52,7 @@ int with_tile(int id, F&& f) {
     case TILE_128x128_W4_K128: return f(Tile<128, 128, 2, 2, 80, 128>{});
     case TILE_64x128_W4_K128: return f(Tile<64, 128, 2, 2, 64, 128>{});
     case TILE_256x256_W8_K64: return f(Tile<256, 256, 2, 4, 160, 64>{});
+    case TILE_64x64_KG4: return f(Tile<64, 64, 2, 1, 132, 128, 4>{});
     default: return f(Tile<64, 128, 2, 2, 53, 64>{});
   }
 }
@@ -108,11 +112,19 @@ int launch_tile(const GemmShape& sh, const Src2& sa, const Src2& sb, const float
     }
   }
   constexpr int nbuf = ring_depth<T, Op, PAIR>();
-  auto kernel = gemm_tile_kernel<Op, T::BM, T::BN, T::WM, T::WN, nbuf, PAIR, Epi>;
-  static int occ = 0;
-  const int grid = persistent_grid(kernel, T::NT, sh.count, occ);
-  hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(T::NT), 0, s, sh, sa, sb, b_scale, epi);
-  return check_launch(what);
+  if constexpr (T::KG > 1) {
+    auto kernel = gemm_splitk_kernel<Op, T::BM, T::BN, T::WM, T::WN, T::KG, nbuf, PAIR, Epi>;
+    static int kocc = 0;
+    const int grid = persistent_grid(kernel, T::NT, sh.count, kocc);
+    hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(T::NT), 0, s, sh, sa, sb, b_scale, epi);
+    return check_launch(what);
+  } else {
+    auto kernel = gemm_tile_kernel<Op, T::BM, T::BN, T::WM, T::WN, nbuf, PAIR, Epi>;
+    static int occ = 0;
+    const int grid = persistent_grid(kernel, T::NT, sh.count, occ);
+    hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(T::NT), 0, s, sh, sa, sb, b_scale, epi);
+    return check_launch(what);
+  }
 }
 
 // Tile plan of one GEMM: the main tile variant and how many of its tiles
@@ -136,7 +148,9 @@ inline int tile_bn(int id) { return with_tile(id, [](auto t) { return decltype(t
 // its whole rounds can run as one launch and the leftover tiles, split into
 // pieces of a smaller variant, as a second launch spread over every CU; the
 // second launch costs about 3 us more (9e6 / K units at ~6 TOP/s per CU).
-// A tile id in the environment variable C4Q_TILE (0..6) forces one launch
+// The split-K 64x64 variant (0.30, one workgroup per CU) only takes such
+// leftover pieces: as the only tile of a GEMM it loses to 64x128.
+// A tile id in the environment variable C4Q_TILE (0..7) forces one launch
 // of that variant, for tuning sweeps.
 inline TilePlan plan_tiles(int64_t M, int64_t N, int64_t K, int cus) {
   const char* env = getenv("C4Q_TILE");
@@ -148,6 +162,9 @@ inline TilePlan plan_tiles(int64_t M, int64_t N, int64_t K, int cus) {
   static const Cand cands[] = {{TILE_256x256_W8, 1, 1.00},
                                {TILE_128x128_W4_K128, 2, 0.87},
                                {TILE_64x128_W4_K128, 2, 0.70}};
+  static const Cand tails[] = {{TILE_128x128_W4_K128, 2, 0.87},
+                               {TILE_64x128_W4_K128, 2, 0.70},
+                               {TILE_64x64_KG4, 1, 0.30}};
   const double gap = 9e6 / (double)(K > 0 ? K : 1);
   TilePlan best{TILE_256x256_W8, 0, -1};
   double best_cost = -1;
@@ -163,7 +180,7 @@ inline TilePlan plan_tiles(int64_t M, int64_t N, int64_t K, int cus) {
     }
     const int64_t whole = tiles / slots * slots, rest = tiles - whole;
     if (whole == 0 || rest == 0) continue;
-    for (const Cand& t : cands) {
+    for (const Cand& t : tails) {
       const int tm = tile_bm(t.id), tn = tile_bn(t.id);
       if (tm * tn >= bm * bn || bm % tm || bn % tn) continue;
       const int64_t pieces = rest * (bm / tm) * (bn / tn);
@@ -209,8 +226,8 @@ inline int plan_launches(int64_t M, int64_t n_rows_b, int64_t N, int64_t K, int 
 template <bool PAIR, class OpFor, class Epi>
 int run_tiles(int64_t M, int64_t n_rows_b, int64_t N, int64_t K, const Src2& sa, const Src2& sb,
               const float* b_scale, const Epi& epi, hipStream_t s, const char* what, OpFor op_for) {
-  // bound on the tile count of any plan (the smallest tile is 64 x 128)
-  C4Q_REQUIRE(cdiv(M, 64) * cdiv(n_rows_b, 128) < (1ll << 27), C4Q_ERR_SHAPE,
+  // bound on the tile count of any plan (the smallest tile is 64 x 64)
+  C4Q_REQUIRE(cdiv(M, 64) * cdiv(n_rows_b, 64) < (1ll << 27), C4Q_ERR_SHAPE,
               "%s: problem too large (%lld x %lld)", what, (long long)M, (long long)n_rows_b);
   int ids[2];
   GemmShape shs[2];

@@ -463,7 +463,7 @@ def _device_plan(M, n_rows_b, K):
     f.argtypes = [ctypes.c_int64] * 3 + [ctypes.c_int, ctypes.c_void_p, ctypes.c_int64,
                                          ctypes.c_void_p]
     cus = torch.cuda.get_device_properties(0).multi_processor_count
-    cover = np.zeros(-(-M // 64) * -(-n_rows_b // 128), np.int32)
+    cover = np.zeros(-(-M // 64) * -(-n_rows_b // 64), np.int32)
     info = np.zeros(8, np.int64)
     assert f(M, n_rows_b, K, cus, cover.ctypes.data, cover.size, info.ctypes.data) == 0
     if info[0] != 2:
@@ -471,7 +471,22 @@ def _device_plan(M, n_rows_b, K):
     return info
 
 
-SPLIT_CASES = [(4352, 512, 4352), (4312, 1040, 4280), (4608, 1024, 4608)]   # 64x128, 64x128, 128x128 pieces
+TILE_SPLIT_K = 7   # 64x64 pieces, K split over 4 wave groups
+
+
+def assert_reordered_sum_close(out, ref, what):
+    """bf16 results of the same products summed in another fp32 order: equal
+    up to the final rounding (one bf16 ulp, 2^-7 relative) plus the fp32
+    reordering error, which matters only where the sum cancels."""
+    o, r = bf16_to_f32(out).astype(np.float64), bf16_to_f32(ref).astype(np.float64)
+    scale = np.abs(r).max() if r.size else 0.0
+    bad = np.abs(o - r) > 2.0 ** -7 * np.abs(r) + 1e-5 * scale
+    assert not bad.any(), f"{what}: {int(bad.sum())} elements differ by more than one ulp"
+
+
+# 64x128, 64x128, 128x128, split-K 64x64 (ragged K), split-K 64x64 (ragged M, N, K) pieces
+SPLIT_CASES = [(4352, 512, 4352), (4312, 1040, 4280), (4608, 1024, 4608), (4352, 1008, 4096),
+               (4300, 1040, 4090)]
 
 
 @pytest.mark.parametrize("M,K,N", SPLIT_CASES)
@@ -494,8 +509,9 @@ def test_split_plan_int8_exact(dev, monkeypatch, M, K, N):
     assert_bits_equal(d, d1, "split plan vs one launch")
 
 
-def test_split_plan_pair_exact(dev, monkeypatch):
-    M, K, N_out = 4352, 512, 2176
+@pytest.mark.parametrize("N_out", [2176, 2048])    # 64x128 pieces, split-K 64x64 pieces
+def test_split_plan_pair_exact(dev, monkeypatch, N_out):
+    M, K = 4352, 512
     _device_plan(M, 2 * N_out, K)
     g = gen(77)
     a, wg, wu = _randint8((M, K), g), _randint8((N_out, K), g), _randint8((N_out, K), g)
@@ -513,7 +529,7 @@ def test_split_plan_pair_exact(dev, monkeypatch):
 
 @pytest.mark.parametrize("M,K,N", SPLIT_CASES)
 def test_split_plan_fp8_and_w8a16(dev, monkeypatch, M, K, N):
-    _device_plan(M, N, K)
+    info = _device_plan(M, N, K)
     g = gen(5 * M + N)
     af = _fp8(torch.randn(M, K, generator=g))
     wf = _fp8(torch.randn(N, K, generator=g) * 0.1)
@@ -536,5 +552,70 @@ def test_split_plan_fp8_and_w8a16(dev, monkeypatch, M, K, N):
                  f"split w8a16 {M}x{K}x{N}")
     monkeypatch.setenv("C4Q_TILE", "0")
     o1, y1 = run()
-    assert_bits_equal(o, o1, "split fp8 vs one launch")
-    assert_bits_equal(y, y1, "split w8a16 vs one launch")
+    if info[3] == TILE_SPLIT_K:
+        assert_reordered_sum_close(o, o1, "split-K fp8 vs one launch")
+        assert_reordered_sum_close(y, y1, "split-K w8a16 vs one launch")
+    else:
+        assert_bits_equal(o, o1, "split fp8 vs one launch")
+        assert_bits_equal(y, y1, "split w8a16 vs one launch")
+
+
+# Whole GEMMs forced through the split-K kernel: K shorter than one stage per
+# group, K not a multiple of the stage, ragged M and N, several pieces per
+# workgroup (M x N beyond one round of 64x64 pieces).
+FORCED_SPLIT_K = [(64, 16, 64), (100, 80, 130), (257, 1008, 190), (1000, 2064, 700),
+                  (2048, 256, 2112)]
+
+
+@pytest.mark.parametrize("M,K,N", FORCED_SPLIT_K)
+def test_forced_split_k_every_family(dev, monkeypatch, M, K, N):
+    g = gen(11 * M + 7 * K + N)
+    a, b = _randint8((M, K), g), _randint8((N, K), g)
+    rs = torch.rand(M, generator=g) * 0.01
+    cs = torch.rand(N, generator=g) * 0.02
+    bb = torch.randn(N, generator=g).to(torch.bfloat16)
+    af = _fp8(torch.randn(M, K, generator=g))
+    wf = _fp8(torch.randn(N, K, generator=g) * 0.1)
+    sa, sb = torch.tensor(0.7), torch.tensor(1.3)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    ws = (wf.float().abs().amax() / 448).reshape(1)
+    ad, bd, afd, wfd, xd = a.to(dev), b.to(dev), af.to(dev), wf.to(dev), x.to(dev)
+
+    def run():
+        c = ops.i8_matmul2d_nt(ad, bd).cpu().numpy()
+        d = bits16(ops.i8_matmul2d_nt_fused_cs(ad, bd, rs.to(dev), cs.to(dev), bb.to(dev)))
+        o = bits16(ops.scaled_mm(afd, wfd.t(), out_dtype=torch.bfloat16, scale_a=sa.to(dev),
+                                 scale_b=sb.to(dev)))
+        y = bits16(ops.w8a16_linear(xd, wfd, ws.to(dev), bb.to(dev)))
+        return c, d, o, y
+
+    monkeypatch.setenv("C4Q_TILE", str(TILE_SPLIT_K))
+    c, d, o, y = run()
+    ref_c = oi.i8_matmul2d_nt(a.numpy(), b.numpy())
+    assert_bits_equal(c, ref_c, f"split-K int32 {M}x{K}x{N}")
+    assert_bits_equal(d, oi.epilogue_rowcolscale(ref_c, rs.numpy(), cs.numpy(), bits16(bb)),
+                      f"split-K fused_cs {M}x{K}x{N}")
+    assert_close(bf16_to_f32(o), bf16_to_f32(of.scaled_mm(u8(af), u8(wf), sa.numpy(), sb.numpy())),
+                 f"split-K fp8 {M}x{K}x{N}")
+    assert_close(bf16_to_f32(y), bf16_to_f32(of.w8a16_linear(bits16(x), u8(wf), ws.numpy(), bits16(bb))),
+                 f"split-K w8a16 {M}x{K}x{N}")
+    monkeypatch.setenv("C4Q_TILE", "0")
+    c0, d0, o0, y0 = run()
+    assert_bits_equal(d, d0, "split-K fused_cs vs 256x256")
+    assert_reordered_sum_close(o, o0, "split-K fp8 vs 256x256")
+    assert_reordered_sum_close(y, y0, "split-K w8a16 vs 256x256")
+
+
+@pytest.mark.parametrize("M,K,N_out", [(100, 80, 96), (600, 1040, 200)])
+def test_forced_split_k_pair(dev, monkeypatch, M, K, N_out):
+    g = gen(3 * M + K + N_out)
+    a, wg, wu = _randint8((M, K), g), _randint8((N_out, K), g), _randint8((N_out, K), g)
+    rs = torch.rand(M, generator=g) * 0.01
+    gs = torch.rand(N_out, generator=g) * 0.02
+    us = torch.rand(N_out, generator=g) * 0.02
+    silu = torch.from_numpy(oact.silu_table().view(np.int16))
+    args = (a.to(dev), wg.to(dev), wu.to(dev), rs.to(dev), gs.to(dev), us.to(dev), silu.to(dev), None)
+    monkeypatch.setenv("C4Q_TILE", str(TILE_SPLIT_K))
+    p = bits16(ops.ffn_pair(*args))
+    assert_bits_equal(p, op.krea2_pair(a.numpy(), wg.numpy(), wu.numpy(), rs.numpy(), gs.numpy(),
+                                       us.numpy()), f"split-K pair {M}x{K}x{N_out}")

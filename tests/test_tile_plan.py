@@ -21,6 +21,7 @@ LIB = NATIVE / "libc4q_probe.so"
 TILE_256 = 0
 TILE_128_K128 = 4
 TILE_64x128_K128 = 5
+TILE_64x64_KG4 = 7
 
 
 @pytest.fixture(scope="module")
@@ -36,7 +37,7 @@ def probe():
 
 
 def plan(probe, M, n_rows_b, K, cus):
-    cover = np.zeros(-(-M // 64) * -(-n_rows_b // 128), np.int32)
+    cover = np.zeros(-(-M // 64) * -(-n_rows_b // 64), np.int32)
     info = np.zeros(8, np.int64)
     assert probe(M, n_rows_b, K, cus, cover.ctypes.data, cover.size, info.ctypes.data) == 0
     return cover, info
@@ -74,12 +75,25 @@ def test_random_shapes_computed_once(probe):
 
 def test_c2_qkv_runs_whole_rounds_then_split_tail(probe):
     """C2 fused QKV on 256 CUs: 36 x 36 = 1296 tiles of 256x256 are five whole
-    rounds (1280 tiles) plus 16; those 16 run as 128 pieces of 64x128."""
+    rounds (1280 tiles) plus 16; those 16 run as 256 split-K pieces of 64x64,
+    one per CU."""
     _, info = plan(probe, 9216, 9216, 3072, 256)
     assert info[0] == 2
     assert (info[1], info[2]) == (TILE_256, 1280)
-    assert (info[3], info[4]) == (TILE_64x128_K128, 16 * 8)
-    assert (info[6], info[7]) == (4, 2)
+    assert (info[3], info[4]) == (TILE_64x64_KG4, 16 * 16)
+    assert (info[6], info[7]) == (4, 4)
+
+
+def test_split_k_tile_is_never_the_main_tile(probe):
+    """The split-K tile only takes leftover pieces (C1's 1024 x 3072 runs as
+    one launch of 64x128 tiles)."""
+    _, info = plan(probe, 1024, 3072, 3072, 256)
+    assert info[0] == 1 and info[1] == TILE_64x128_K128
+    rng = np.random.default_rng(1)
+    for _ in range(200):
+        M, NB = int(rng.integers(1, 20000)), int(rng.integers(1, 20000))
+        _, info = plan(probe, M, NB, 3072, 256)
+        assert info[1] != TILE_64x64_KG4, (M, NB, info.tolist())
 
 
 def test_whole_rounds_need_no_tail(probe):
