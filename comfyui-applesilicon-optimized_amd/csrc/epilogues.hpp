@@ -20,6 +20,13 @@
 //   value4(m, n, v, nv)        = apply(rowp(m), col(n, nv), v)
 //   row(m), vec                byte pointer to output row m; rows are
 //                              16-byte aligned (chunked stores allowed)
+//   kColFields, col_raw(f, n, N), col_val(f, w), row_raw(m, M)
+//                              the same parameters as raw words, one column
+//                              or row per call: col_raw / row_raw only load
+//                              (buffer loads: reads past N or M return 0),
+//                              col_val converts field f of a loaded word;
+//                              col(n, nv) field f, element q equals
+//                              col_val(f, col_raw(f, n + q, N)) for q < nv
 // The tiled kernels load a lane's column parameters once per tile and its
 // row parameters once per 32-row block, so the store loop does no loads
 // besides activation-table lookups.
@@ -69,6 +76,29 @@ __device__ __forceinline__ float raw_f32(uint32_t raw, int dt) {
   return __builtin_bit_cast(float, raw);
 }
 
+// Raw parameter words through buffer resources over [p, p + n elements):
+// loads only (reads past the range return 0), so that a caller can issue
+// them long before it converts them.
+__device__ __forceinline__ uint32_t raw_load32(const void* p, int64_t n, int64_t i) {
+  const int64_t bytes = p ? n * 4 : 0;
+  const int32_t range = bytes > 0x7FFFFFF0ll ? 0x7FFFFFF0 : (int32_t)bytes;
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, range, 0x00020000);
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)(i * 4), 0, 0);
+}
+__device__ __forceinline__ uint32_t raw_load16(const void* p, int64_t n, int64_t i) {
+  const int64_t bytes = p ? n * 2 : 0;
+  const int32_t range = bytes > 0x7FFFFFF0ll ? 0x7FFFFFF0 : (int32_t)bytes;
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, range, 0x00020000);
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)(i * 2), 0, 0);
+}
+// A bias / scale element of dtype dt (DT_F32 or a 16-bit type), raw.
+__device__ __forceinline__ uint32_t raw_load_dt(const void* p, int dt, int64_t n, int64_t i) {
+  if (dt == DT_F32) return raw_load32(p, n, i);
+  return raw_load16(p, n, i);
+}
+
 template <class T>
 struct EpiOut {
   using OutT = T;
@@ -95,6 +125,10 @@ struct EpiI32 : EpiOut<uint32_t> {
   __device__ __forceinline__ EpiI32 prepare() const { return *this; }
   __device__ __forceinline__ Col col(int64_t, int) const { return {}; }
   __device__ __forceinline__ float rowp(int64_t) const { return 0.0f; }
+  static constexpr int kColFields = 0;
+  __device__ __forceinline__ uint32_t col_raw(int, int64_t, int64_t) const { return 0; }
+  __device__ __forceinline__ float col_val(int, uint32_t) const { return 0.0f; }
+  __device__ __forceinline__ uint32_t row_raw(int64_t, int64_t) const { return 0; }
   __device__ __forceinline__ uint4 apply(float, const Col&, const int32_t (&v)[4]) const {
     return uint4{(uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]};
   }
@@ -117,6 +151,10 @@ struct EpiRowScale : EpiOut<uint16_t> {
     return c;
   }
   __device__ __forceinline__ float rowp(int64_t m) const { return rs[m]; }
+  static constexpr int kColFields = 1;
+  __device__ __forceinline__ uint32_t col_raw(int, int64_t n, int64_t N) const { return raw_load16(bias, N, n); }
+  __device__ __forceinline__ float col_val(int, uint32_t w) const { return bias ? bf16_f32((uint16_t)w) : 0.0f; }
+  __device__ __forceinline__ uint32_t row_raw(int64_t m, int64_t M) const { return raw_load32(rs, M, m); }
   __device__ __forceinline__ uint2 apply(float r, const Col& c, const int32_t (&v)[4]) const {
     uint2 p = pack_bf16x4<uint2>((float)v[0] * r, (float)v[1] * r, (float)v[2] * r, (float)v[3] * r);
     if (bias)
@@ -146,6 +184,14 @@ struct EpiRowColScale : EpiOut<uint16_t> {
     return c;
   }
   __device__ __forceinline__ float rowp(int64_t m) const { return rs[m]; }
+  static constexpr int kColFields = 2;   // s, b
+  __device__ __forceinline__ uint32_t col_raw(int f, int64_t n, int64_t N) const {
+    return f == 0 ? raw_load32(cs, N, n) : raw_load16(bias, N, n);
+  }
+  __device__ __forceinline__ float col_val(int f, uint32_t w) const {
+    return f == 0 ? bits_f32(w) : (bias ? bf16_f32((uint16_t)w) : 0.0f);
+  }
+  __device__ __forceinline__ uint32_t row_raw(int64_t m, int64_t M) const { return raw_load32(rs, M, m); }
   __device__ __forceinline__ uint2 apply(float r, const Col& c, const int32_t (&v)[4]) const {
     float x[4];
 #pragma unroll
@@ -196,6 +242,18 @@ struct EpiScaled : EpiOut<typename std::conditional<F32OUT, uint32_t, uint16_t>:
     return c;
   }
   __device__ __forceinline__ float rowp(int64_t m) const { return sa[m * sa_step]; }
+  static constexpr int kColFields = 2;   // s, b
+  __device__ __forceinline__ uint32_t col_raw(int f, int64_t n, int64_t N) const {
+    if (f == 0) return raw_load32(sb, sb_step ? N : 1, n * sb_step);
+    return raw_load_dt(bias, bias_dt, N, n);
+  }
+  __device__ __forceinline__ float col_val(int f, uint32_t w) const {
+    if (f == 0) return bits_f32(w);
+    return bias ? raw_f32(w, bias_dt) : 0.0f;
+  }
+  __device__ __forceinline__ uint32_t row_raw(int64_t m, int64_t M) const {
+    return raw_load32(sa, sa_step ? M : 1, m * sa_step);
+  }
   __device__ __forceinline__ Packed apply(float a, const Col& c, const float (&v)[4]) const {
     float o[4];
 #pragma unroll
@@ -235,6 +293,12 @@ struct EpiW8A16 : EpiOut<typename std::conditional<F32OUT, uint32_t, uint16_t>::
     return c;
   }
   __device__ __forceinline__ float rowp(int64_t) const { return 0.0f; }
+  static constexpr int kColFields = 1;
+  __device__ __forceinline__ uint32_t col_raw(int, int64_t n, int64_t N) const {
+    return raw_load_dt(bias, bias_dt, N, n);
+  }
+  __device__ __forceinline__ float col_val(int, uint32_t w) const { return bias ? raw_f32(w, bias_dt) : 0.0f; }
+  __device__ __forceinline__ uint32_t row_raw(int64_t, int64_t) const { return 0; }
   __device__ __forceinline__ Packed apply(float, const Col& c, const float (&v)[4]) const {
     float o[4] = {v[0], v[1], v[2], v[3]};
     if (bias) {
@@ -280,6 +344,12 @@ struct EpiPair : EpiOut<uint16_t> {
     return c;
   }
   __device__ __forceinline__ float rowp(int64_t m) const { return rs[m]; }
+  static constexpr int kColFields = 2;   // s1, s2
+  __device__ __forceinline__ uint32_t col_raw(int f, int64_t n, int64_t N) const {
+    return raw_load32(f == 0 ? s1 : s2, N, n);
+  }
+  __device__ __forceinline__ float col_val(int, uint32_t w) const { return bits_f32(w); }
+  __device__ __forceinline__ uint32_t row_raw(int64_t m, int64_t M) const { return raw_load32(rs, M, m); }
   __device__ __forceinline__ uint2 apply(float r, const Col& c, const int32_t (&g)[4],
                                          const int32_t (&u)[4]) const {
     float a[4], b[4];

@@ -495,9 +495,89 @@ __device__ __forceinline__ void load_rows(const Epi& epi, int64_t m0, int64_t M,
     }
 }
 
-template <int TM, int TN, class Acc, class Epi>
+// The epilogue parameters of one wave's sub-tile: its lanes' column groups
+// and rows (loaded by load(), or ahead of the epilogue by the kernel).
+template <int TM, int TN, bool PAIR, class Epi>
+struct EpiParams {
+  static constexpr int COLS = PAIR ? TN / 2 * 32 : TN * 32;
+  using Map = StoreMap<COLS, typename Epi::OutT>;
+  typename Epi::Col col[Map::NG];
+  float rp[TM][4];
+  // n0: first output column of the sub-tile (pair: first output column)
+  __device__ __forceinline__ void load(const Epi& epi, int64_t m0, int64_t n0, int64_t M,
+                                       int64_t N) {
+    const int lane = threadIdx.x & 63;
+    load_cols<Map>(epi, n0, N, lane, col);
+    load_rows<TM>(epi, m0, M, lane >> 3, rp);
+  }
+};
+
+// The same parameters in compact raw form, for loading early: lane l holds
+// the raw words of column n0 + l and of rows m0 + l + 64 r. Loading issues
+// buffer loads only; nothing reads the words until settle(), so the loads
+// are waited for where settle() stands. expand() then spreads them to the
+// lanes that use them with cross-lane reads (ds_bpermute: LDS hardware, no
+// memory wait) and converts them.
+template <int TM, int TN, bool PAIR, class Epi>
+struct EpiParamsEarly {
+  using Full = EpiParams<TM, TN, PAIR, Epi>;
+  static constexpr int F = Epi::kColFields;
+  static constexpr int CW = (Full::COLS + 63) / 64;
+  static constexpr int RR = (TM * 32 + 63) / 64;
+  static_assert(F == 0 || (int)sizeof(typename Epi::Col) == F * 16, "Col is float[F][4]");
+  uint32_t cw[F > 0 ? F : 1][CW];
+  uint32_t rw[RR];
+  __device__ __forceinline__ void load(const Epi& epi, int64_t m0, int64_t n0, int64_t M,
+                                       int64_t N) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int f = 0; f < F; ++f)
+#pragma unroll
+      for (int w = 0; w < CW; ++w) cw[f][w] = epi.col_raw(f, n0 + lane + 64 * w, N);
+#pragma unroll
+    for (int r = 0; r < RR; ++r) rw[r] = epi.row_raw(m0 + lane + 64 * r, M);
+  }
+  __device__ __forceinline__ void settle() {
+#pragma unroll
+    for (int f = 0; f < F; ++f)
+#pragma unroll
+      for (int w = 0; w < CW; ++w) asm volatile("" : "+v"(cw[f][w]));
+#pragma unroll
+    for (int r = 0; r < RR; ++r) asm volatile("" : "+v"(rw[r]));
+  }
+  __device__ __forceinline__ void expand(const Epi& epi, Full& out) const {
+    using Map = typename Full::Map;
+    const int lane = threadIdx.x & 63, prow = lane >> 3;
+    if constexpr (F > 0) {
+#pragma unroll
+      for (int g = 0; g < Map::NG; ++g) {
+        // a group's columns lie in one 64-column word: w is the same for
+        // every lane (unit starts are UNIT * 8 apart, UNIT * 8 <= 64)
+        const int w = (Map::UNIT * 8 * (g / Map::GPU)) >> 6;
+        struct { float v[F][4]; } c;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int src = Map::col(lane, g) + q - 64 * w;
+#pragma unroll
+          for (int f = 0; f < F; ++f) c.v[f][q] = epi.col_val(f, (uint32_t)__shfl((int)cw[f][w], src));
+        }
+        out.col[g] = __builtin_bit_cast(typename Epi::Col, c);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r0 = i * 32 + q * 8;              // + prow < 8: stays in one 64-row word
+        out.rp[i][q] = bits_f32((uint32_t)__shfl((int)rw[r0 >> 6], (r0 & 63) + prow));
+      }
+  }
+};
+
+template <int TM, int TN, class Acc, class Epi, class Params>
 __device__ __forceinline__ void epilogue_single(const Acc (&acc)[TM][TN], int64_t m0, int64_t n0,
-                                                int64_t M, int64_t N, const Epi& epi, uint8_t* lds) {
+                                                int64_t M, int64_t N, const Epi& epi, uint8_t* lds,
+                                                const Params& pr) {
   using Scalar = std::remove_cv_t<std::remove_reference_t<decltype(acc[0][0][0])>>;
   constexpr int COLS = TN * 32;
   using Map = StoreMap<COLS, typename Epi::OutT>;
@@ -505,10 +585,8 @@ __device__ __forceinline__ void epilogue_single(const Acc (&acc)[TM][TN], int64_
   using Packed = typename Epi::Packed;
   Scalar* sw = reinterpret_cast<Scalar*>(lds);
   const int lane = threadIdx.x & 63, prow = lane >> 3;
-  typename Epi::Col col[Map::NG];
-  load_cols<Map>(epi, n0, N, lane, col);
-  float rp[TM][4];
-  load_rows<TM>(epi, m0, M, prow, rp);
+  const auto& col = pr.col;
+  const auto& rp = pr.rp;
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
 #pragma unroll
@@ -543,18 +621,17 @@ __device__ __forceinline__ void epilogue_single(const Acc (&acc)[TM][TN], int64_
 
 // Pair epilogue: blocks 2t (gate) and 2t+1 (up) give the same 32 output
 // columns c0 + 32 t + lane%32; the strip interleaves them per column.
-template <int TM, int TN, class Acc, class Epi>
+template <int TM, int TN, class Acc, class Epi, class Params>
 __device__ __forceinline__ void epilogue_pair(const Acc (&acc)[TM][TN], int64_t m0, int64_t c0,
-                                              int64_t M, int64_t NC, const Epi& epi, uint8_t* lds) {
+                                              int64_t M, int64_t NC, const Epi& epi, uint8_t* lds,
+                                              const Params& pr) {
   constexpr int COLS = TN / 2 * 32;
   using Map = StoreMap<COLS, typename Epi::OutT>;
   using St = Strip<2 * COLS>;
   int32_t* sw = reinterpret_cast<int32_t*>(lds);
   const int lane = threadIdx.x & 63, prow = lane >> 3;
-  typename Epi::Col col[Map::NG];
-  load_cols<Map>(epi, c0, NC, lane, col);
-  float rp[TM][4];
-  load_rows<TM>(epi, m0, M, prow, rp);
+  const auto& col = pr.col;
+  const auto& rp = pr.rp;
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
 #pragma unroll
@@ -653,7 +730,7 @@ gemm_tile_kernel(GemmShape sh, Src2 sa, Src2 sb, const float* b_scale, Epi epi) 
   const int G = (int)gridDim.x;
   const int my_tiles = (ntiles - 1 - (int)blockIdx.x) / G + 1;
   const Epi ep = epi.prepare();
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform
   const int wm = wave / WN, wn = wave % WN;
   const float ws = Op::prep_scale(b_scale);
 
@@ -668,7 +745,7 @@ gemm_tile_kernel(GemmShape sh, Src2 sa, Src2 sb, const float* b_scale, Epi epi) 
   // Copy cursor: next stage to issue is stage ips of this workgroup's tile ij.
   int ij = 0, ips = 0;
   u32x4 ra, rb0, rb1;
-  auto tile_rsrc = [&](int j) {
+  auto tile_rsrc = [&](int j) __attribute__((always_inline)) {
     const TileCoord tc = tile_at(sh, (int)blockIdx.x + j * G);
     const int64_t m0 = (int64_t)tc.tm * BM;
     const int64_t brow0 = PAIR ? ((int64_t)tc.tn * BN >> 1) : (int64_t)tc.tn * BN;
@@ -680,7 +757,7 @@ gemm_tile_kernel(GemmShape sh, Src2 sa, Src2 sb, const float* b_scale, Epi epi) 
   // Issue the next stage into `buf`; past this workgroup's last tile the
   // copies read zeros (every stage issues the same number of copies, which
   // keeps the vmcnt arithmetic fixed).
-  auto issue_next = [&](uint8_t* buf) {
+  auto issue_next = [&](uint8_t* buf) __attribute__((always_inline)) {
     if (ij < my_tiles) {
       la.issue(ra, ra, buf, ips * SA, a_kb);
       lb.issue(rb0, rb1, buf + BM * SA, ips * SB, b_kb);
@@ -723,16 +800,35 @@ gemm_tile_kernel(GemmShape sh, Src2 sa, Src2 sb, const float* b_scale, Epi epi) 
       const uint8_t* cur = smem + (gs % NBUF) * STAGE;
       Op::template frags<TM, TN>(fr[0], cur, cur + BM * SA, ra0, rb0i, 0);
     }
-    for (int st = 0; st < nst; ++st, ++gs) {
+    const TileCoord tc = tile_at(sh, (int)blockIdx.x + j * G);
+    const int64_t wm0 = (int64_t)tc.tm * BM + wm * (TM * 32);
+    const int64_t wn0 = PAIR ? ((int64_t)tc.tn * BN >> 1) + wn * (TN * 16)
+                             : (int64_t)tc.tn * BN + wn * (TN * 32);
+    EpiParams<TM, TN, PAIR, Epi> prm;
+    EpiParamsEarly<TM, TN, PAIR, Epi> early;
+    // One stage; LAST: the tile's last stage, after which the epilogue runs.
+    // With a two-stage ring every stage ends by waiting for all of this
+    // wave's copies (vmcnt(0)). The last stage then loads the epilogue
+    // parameters (raw, compact) first and settles them right after that
+    // wait, before the next tile's first copies are issued: loaded later,
+    // they would be newer than those copies, and their first use would wait
+    // for the copies too (memory counters complete in issue order).
+    // (Only where the early parameters fit: at most 8 accumulator blocks per
+    // wave; larger wave tiles keep one loop and load them at the epilogue.)
+    constexpr bool kEarlyParams = NBUF == 2 && TM * TN <= 8;
+    auto stage = [&](auto last, bool has_next) __attribute__((always_inline)) {
+      constexpr bool kEarly = decltype(last)::value && kEarlyParams;
+      if constexpr (kEarly) early.load(ep, wm0, wn0, sh.M, PAIR ? sh.N >> 1 : sh.N);
       uint8_t* cur = smem + (gs % NBUF) * STAGE;
       const uint8_t* nxt = smem + ((gs + 1) % NBUF) * STAGE;
 #pragma unroll
       for (int s = 0; s < S; ++s) {
         if (s == S - 1) {
           wait_vm<(NBUF - 2) * kPerStage>();   // this wave's copies of stage gs+1 landed
+          if constexpr (kEarly) early.settle();
           stage_barrier();                     // ... and every wave's; stage gs fully read
           issue_next(cur);                     // refill with stage gs+NBUF
-          if (st + 1 < nst) Op::template frags<TM, TN>(fr[0], nxt, nxt + BM * SA, ra0, rb0i, 0);
+          if (has_next) Op::template frags<TM, TN>(fr[0], nxt, nxt + BM * SA, ra0, rb0i, 0);
         } else {
           Op::template frags<TM, TN>(fr[(s + 1) & 1], cur, cur + BM * SA, ra0, rb0i, s + 1);
           // keep the next step's LDS reads ahead of this step's MFMAs: left to
@@ -742,14 +838,20 @@ gemm_tile_kernel(GemmShape sh, Src2 sa, Src2 sb, const float* b_scale, Epi epi) 
         }
         Op::template mma<TM, TN>(fr[s & 1], acc, ws);
       }
-    }
-    const TileCoord tc = tile_at(sh, (int)blockIdx.x + j * G);
-    const int64_t wm0 = (int64_t)tc.tm * BM + wm * (TM * 32);
-    if constexpr (PAIR) {
-      const int64_t c0 = ((int64_t)tc.tn * BN >> 1) + wn * (TN * 16);
-      epilogue_pair<TM, TN>(acc, wm0, c0, sh.M, sh.N >> 1, ep, strip);
+      ++gs;
+    };
+    if constexpr (kEarlyParams) {
+      for (int st = 0; st + 1 < nst; ++st) stage(std::false_type{}, true);
+      stage(std::true_type{}, false);
+      early.expand(ep, prm);
     } else {
-      epilogue_single<TM, TN>(acc, wm0, (int64_t)tc.tn * BN + wn * (TN * 32), sh.M, sh.N, ep, strip);
+      for (int st = 0; st < nst; ++st) stage(std::false_type{}, st + 1 < nst);
+      prm.load(ep, wm0, wn0, sh.M, PAIR ? sh.N >> 1 : sh.N);
+    }
+    if constexpr (PAIR) {
+      epilogue_pair<TM, TN>(acc, wm0, wn0, sh.M, sh.N >> 1, ep, strip, prm);
+    } else {
+      epilogue_single<TM, TN>(acc, wm0, wn0, sh.M, sh.N, ep, strip, prm);
     }
   }
   wait_vm<0>();    // zero-fill copies past the last tile still target the ring
@@ -811,7 +913,7 @@ gemm_pingpong_kernel(GemmShape sh, Src2 sa, Src2 sb, const float* b_scale, Epi e
 
   int ij = 0, ips = 0;
   u32x4 ra, rb0, rb1;
-  auto tile_rsrc = [&](int j) {
+  auto tile_rsrc = [&](int j) __attribute__((always_inline)) {
     const TileCoord tc = tile_at(sh, (int)blockIdx.x + j * G);
     const int64_t m0 = (int64_t)tc.tm * BM;
     const int64_t brow0 = PAIR ? ((int64_t)tc.tn * BN >> 1) : (int64_t)tc.tn * BN;
@@ -820,7 +922,7 @@ gemm_pingpong_kernel(GemmShape sh, Src2 sa, Src2 sb, const float* b_scale, Epi e
     rb0 = dma_rsrc(sb.p0 + brow0 * sb.ld_bytes, bleft);
     rb1 = PAIR ? dma_rsrc(sb.p1 + brow0 * sb.ld_bytes, bleft) : rb0;
   };
-  auto issue_next = [&](uint8_t* buf) {
+  auto issue_next = [&](uint8_t* buf) __attribute__((always_inline)) {
     if (ij < my_tiles) {
       la.issue(ra, ra, buf, ips * SA, a_kb);
       lb.issue(rb0, rb1, buf + BM * SA, ips * SB, b_kb);
@@ -877,11 +979,14 @@ gemm_pingpong_kernel(GemmShape sh, Src2 sa, Src2 sb, const float* b_scale, Epi e
     }
     const TileCoord tc = tile_at(sh, (int)blockIdx.x + j * G);
     const int64_t wm0 = (int64_t)tc.tm * BM + grp * (TM * 32);
+    const int64_t wn0 = PAIR ? ((int64_t)tc.tn * BN >> 1) + wn * (TN * 16)
+                             : (int64_t)tc.tn * BN + wn * (TN * 32);
+    EpiParams<TM, TN, PAIR, Epi> prm;
+    prm.load(ep, wm0, wn0, sh.M, PAIR ? sh.N >> 1 : sh.N);
     if constexpr (PAIR) {
-      const int64_t c0 = ((int64_t)tc.tn * BN >> 1) + wn * (TN * 16);
-      epilogue_pair<TM, TN>(acc, wm0, c0, sh.M, sh.N >> 1, ep, strip);
+      epilogue_pair<TM, TN>(acc, wm0, wn0, sh.M, sh.N >> 1, ep, strip, prm);
     } else {
-      epilogue_single<TM, TN>(acc, wm0, (int64_t)tc.tn * BN + wn * (TN * 32), sh.M, sh.N, ep, strip);
+      epilogue_single<TM, TN>(acc, wm0, wn0, sh.M, sh.N, ep, strip, prm);
     }
   }
   if (grp == 0) stage_barrier();               // matches group 1's extra barrier
@@ -954,7 +1059,7 @@ gemm_splitk_kernel(GemmShape sh, Src2 sa, Src2 sb, const float* b_scale, Epi epi
     const u32x4 rb1 = PAIR ? dma_rsrc(sb.p1 + brow0 * sb.ld_bytes, bleft) : rb0;
     // stage s of this group: K block s * KG + grp (zeros past K, so every
     // stage issues the same copies and the vmcnt arithmetic stays fixed)
-    auto issue = [&](int s) {
+    auto issue = [&](int s) __attribute__((always_inline)) {
       uint8_t* buf = smem + (s % NBUF) * STAGE + grp * SUB;
       const int blk = s * KG + grp;
       la.issue(ra, ra, buf, blk * SA, a_kb);
@@ -1019,11 +1124,13 @@ gemm_splitk_kernel(GemmShape sh, Src2 sa, Src2 sb, const float* b_scale, Epi epi
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][jj][r] += part[slot(g, i, jj, r)];
       const int64_t wm0 = m0 + wm * (TM * 32);
+      const int64_t wn0 = brow0 + wn * (PAIR ? TN * 16 : TN * 32);
+      EpiParams<TM, TN, PAIR, Epi> prm;
+      prm.load(ep, wm0, wn0, sh.M, PAIR ? sh.N >> 1 : sh.N);
       if constexpr (PAIR) {
-        const int64_t c0 = brow0 + wn * (TN * 16);
-        epilogue_pair<TM, TN>(acc, wm0, c0, sh.M, sh.N >> 1, ep, strip);
+        epilogue_pair<TM, TN>(acc, wm0, wn0, sh.M, sh.N >> 1, ep, strip, prm);
       } else {
-        epilogue_single<TM, TN>(acc, wm0, brow0 + wn * (TN * 32), sh.M, sh.N, ep, strip);
+        epilogue_single<TM, TN>(acc, wm0, wn0, sh.M, sh.N, ep, strip, prm);
       }
     }
     stage_barrier();                           // partial sums read before the ring refills
