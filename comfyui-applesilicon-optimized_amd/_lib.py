@@ -28,6 +28,7 @@ _SIGNATURES = {
     "c4q_i8_gemm_nt_i32": [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P],
     "c4q_i8_gemm_nt_fused": [_P, _I64, _P, _I64, _P, _I64, _P, _P, _I64, _I64, _I64, _P],
     "c4q_i8_gemm_nt_fused_cs": [_P, _I64, _P, _I64, _P, _I64, _P, _P, _P, _I64, _I64, _I64, _P],
+    "c4q_i8_gemm_nt_fused_cs_f16": [_P, _I64, _P, _I64, _P, _I64, _P, _P, _P, _I64, _I64, _I64, _P],
     "c4q_i8_quant_rowwise": [_P, _I, _I64, _P, _I64, _P, _I64, _I64, _P],
     "c4q_f8_gemm_nt_scaled": [_P, _I64, _P, _I64, _P, _I, _I64, _P, _I, _P, _I, _P, _P, _I,
                               _I64, _I64, _I64, _P],
@@ -37,6 +38,7 @@ _SIGNATURES = {
                           _I64, _I64, _I64, _P],
     "c4q_i8_ffn_pair": [_P, _I64, _P, _P, _I64, _P, _I64, _P, _P, _P, _P, _P,
                         _I64, _I64, _I64, _P],
+    "c4q_bf16_ffn_pair": [_P, _I64, _P, _P, _I64, _P, _I64, _P, _P, _I64, _I64, _I64, _P],
 }
 
 _lib = None

@@ -54,8 +54,12 @@ __device__ __forceinline__ uint32_t bf16x2_rne(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, h);
 }
 // Two floats to packed IEEE half, round to nearest even (v_cvt_f16_f32;
-// checked the same way against f16_rte).
+// checked the same way against f16_rte). The empty asm makes the two f32
+// values exist as written: otherwise the compiler fuses the f32 multiply or
+// add that produced them into v_fma_mixlo_f16, which rounds the exact result
+// to half once instead of to f32 first (a different half at f32 ties).
 __device__ __forceinline__ uint32_t f16x2_rne(float lo, float hi) {
+  asm("" : "+v"(lo), "+v"(hi));
   return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)lo) |
          ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)hi) << 16);
 }
@@ -168,18 +172,22 @@ struct EpiRowScale : EpiOut<uint16_t> {
 };
 
 // Per-channel fused dequant: s = col_scale[n] * row_scale[m] first, then
-// D = bf16(f32(C) * s), optional bias as above
-// (reference _patches/int8_ext/int8_gemm.mm:417-443).
-struct EpiRowColScale : EpiOut<uint16_t> {
+// D = T(f32(C) * s), optional bias as a second rounding T(f32(D) + f32(bias[n]))
+// with T = bf16 (reference _patches/int8_ext/int8_gemm.mm:417-443) or, F16,
+// IEEE half with a half bias (the fp16 epilogue nax_frag_store_dequant_cs_half,
+// _patches/int8_ext/int8_gemm.mm:1161-1183).
+template <bool F16>
+struct EpiRowColScaleT : EpiOut<uint16_t> {
   const float* rs; const float* cs; const uint16_t* bias;
   struct Col { float s[4], b[4]; };
-  __device__ __forceinline__ EpiRowColScale prepare() const { return *this; }
+  __device__ __forceinline__ static float out_f32(uint16_t h) { return F16 ? f16_f32(h) : bf16_f32(h); }
+  __device__ __forceinline__ EpiRowColScaleT prepare() const { return *this; }
   __device__ __forceinline__ Col col(int64_t n, int nv) const {
     Col c;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       c.s[q] = cs[colq(n, q, nv)];
-      c.b[q] = bias ? bf16_f32(bias[colq(n, q, nv)]) : 0.0f;
+      c.b[q] = bias ? out_f32(bias[colq(n, q, nv)]) : 0.0f;
     }
     return c;
   }
@@ -189,23 +197,30 @@ struct EpiRowColScale : EpiOut<uint16_t> {
     return f == 0 ? raw_load32(cs, N, n) : raw_load16(bias, N, n);
   }
   __device__ __forceinline__ float col_val(int f, uint32_t w) const {
-    return f == 0 ? bits_f32(w) : (bias ? bf16_f32((uint16_t)w) : 0.0f);
+    return f == 0 ? bits_f32(w) : (bias ? out_f32((uint16_t)w) : 0.0f);
   }
   __device__ __forceinline__ uint32_t row_raw(int64_t m, int64_t M) const { return raw_load32(rs, M, m); }
+  __device__ __forceinline__ static uint2 pack(float a, float b, float c, float d) {
+    if constexpr (F16) return uint2{f16x2_rne(a, b), f16x2_rne(c, d)};
+    return pack_bf16x4<uint2>(a, b, c, d);
+  }
   __device__ __forceinline__ uint2 apply(float r, const Col& c, const int32_t (&v)[4]) const {
     float x[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) x[q] = (float)v[q] * (c.s[q] * r);
-    uint2 p = pack_bf16x4<uint2>(x[0], x[1], x[2], x[3]);
+    uint2 p = pack(x[0], x[1], x[2], x[3]);
     if (bias)
-      p = pack_bf16x4<uint2>(bf16lo(p.x) + c.b[0], bf16hi(p.x) + c.b[1], bf16lo(p.y) + c.b[2],
-                             bf16hi(p.y) + c.b[3]);
+      p = pack(out_f32((uint16_t)p.x) + c.b[0], out_f32((uint16_t)(p.x >> 16)) + c.b[1],
+               out_f32((uint16_t)p.y) + c.b[2], out_f32((uint16_t)(p.y >> 16)) + c.b[3]);
     return p;
   }
   __device__ __forceinline__ uint2 value4(int64_t m, int64_t n, const int32_t (&v)[4], int nv) const {
     return apply(rowp(m), col(n, nv), v);
   }
 };
+
+using EpiRowColScale = EpiRowColScaleT<false>;
+using EpiRowColScaleF16 = EpiRowColScaleT<true>;
 
 // torch._scaled_mm on the fp8 route: out = f32 acc, then * scale_a,
 // * scale_b, * scale_result, + f32(bias), each in f32 and in this order,
@@ -373,6 +388,41 @@ struct EpiPair : EpiOut<uint16_t> {
   }
   __device__ __forceinline__ uint2 pair4(int64_t m, int64_t n, const int32_t (&g)[4],
                                          const int32_t (&u)[4], int nv) const {
+    return apply(rowp(m), col(n, nv), g, u);
+  }
+};
+
+// MOSS bf16 FC1/SiTU pair on fp32 accumulators of a bf16 x bf16 GEMM, no
+// scales: x1 = bf16(acc_h), x2 = bf16(acc_g), out = bf16(f32(T1[x1]) *
+// f32(T2[x2])) (missing table = identity)
+// (reference _patches/moss_bf16_ffn_pair.metal:282-304).
+struct EpiPairF : EpiOut<uint16_t> {
+  const uint16_t* t1; const uint16_t* t2;
+  struct Col {};
+  __device__ __forceinline__ EpiPairF prepare() const { return *this; }
+  __device__ __forceinline__ Col col(int64_t, int) const { return {}; }
+  __device__ __forceinline__ float rowp(int64_t) const { return 0.0f; }
+  static constexpr int kColFields = 0;
+  __device__ __forceinline__ uint32_t col_raw(int, int64_t, int64_t) const { return 0; }
+  __device__ __forceinline__ float col_val(int, uint32_t) const { return 0.0f; }
+  __device__ __forceinline__ uint32_t row_raw(int64_t, int64_t) const { return 0; }
+  __device__ __forceinline__ uint2 apply(float, const Col&, const float (&g)[4],
+                                         const float (&u)[4]) const {
+    uint2 x1 = pack_bf16x4<uint2>(g[0], g[1], g[2], g[3]);
+    uint2 x2 = pack_bf16x4<uint2>(u[0], u[1], u[2], u[3]);
+    if (t1) {
+      x1.x = (uint32_t)t1[x1.x & 0xFFFFu] | ((uint32_t)t1[x1.x >> 16] << 16);
+      x1.y = (uint32_t)t1[x1.y & 0xFFFFu] | ((uint32_t)t1[x1.y >> 16] << 16);
+    }
+    if (t2) {
+      x2.x = (uint32_t)t2[x2.x & 0xFFFFu] | ((uint32_t)t2[x2.x >> 16] << 16);
+      x2.y = (uint32_t)t2[x2.y & 0xFFFFu] | ((uint32_t)t2[x2.y >> 16] << 16);
+    }
+    return pack_bf16x4<uint2>(bf16lo(x1.x) * bf16lo(x2.x), bf16hi(x1.x) * bf16hi(x2.x),
+                              bf16lo(x1.y) * bf16lo(x2.y), bf16hi(x1.y) * bf16hi(x2.y));
+  }
+  __device__ __forceinline__ uint2 pair4(int64_t m, int64_t n, const float (&g)[4],
+                                         const float (&u)[4], int nv) const {
     return apply(rowp(m), col(n, nv), g, u);
   }
 };

@@ -351,6 +351,36 @@ struct OpW8A16 {
   }
 };
 
+// bf16 x bf16 -> fp32, v_mfma_f32_32x32x16_bf16 (the MOSS bf16 FFN pair):
+// both operands staged as 128-byte rows (64 K values); a lane holds 8 K
+// values (one chunk), so a stage is 4 K steps of one MFMA each, in natural K
+// order on both operands (step s, lane half h: chunk 2s + h).
+struct OpBF16T {
+  using Acc = f32x16;
+  static constexpr int kStageK = 64, SA = 128, SB = 128, S = 4;
+  static constexpr bool kPingPong = false;
+  template <int TM, int TN> struct Frag { i32x4 a[TM], b[TN]; };
+  __device__ __forceinline__ static float prep_scale(const float*) { return 1.0f; }
+  template <int TM, int TN>
+  __device__ __forceinline__ static void frags(Frag<TM, TN>& f, const uint8_t* sa, const uint8_t* sb,
+                                               int ra0, int rb0, int s) {
+    const int lane = threadIdx.x & 63, lr = lane & 31, h = lane >> 5;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) f.a[i] = lds_chunk<SA>(sa, ra0 + i * 32 + lr, 2 * s + h);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) f.b[j] = lds_chunk<SB>(sb, rb0 + j * 32 + lr, 2 * s + h);
+  }
+  template <int TM, int TN>
+  __device__ __forceinline__ static void mma(const Frag<TM, TN>& f, Acc (&acc)[TM][TN], float) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bitcast<bf16x8>(f.a[i]),
+                                                            bitcast<bf16x8>(f.b[j]), acc[i][j], 0, 0, 0);
+  }
+};
+
 // ----------------------------------------------------- tile scheduling ---
 struct TileCoord { int tm, tn; };
 
@@ -625,10 +655,11 @@ template <int TM, int TN, class Acc, class Epi, class Params>
 __device__ __forceinline__ void epilogue_pair(const Acc (&acc)[TM][TN], int64_t m0, int64_t c0,
                                               int64_t M, int64_t NC, const Epi& epi, uint8_t* lds,
                                               const Params& pr) {
+  using Scalar = std::remove_cv_t<std::remove_reference_t<decltype(acc[0][0][0])>>;
   constexpr int COLS = TN / 2 * 32;
   using Map = StoreMap<COLS, typename Epi::OutT>;
   using St = Strip<2 * COLS>;
-  int32_t* sw = reinterpret_cast<int32_t*>(lds);
+  Scalar* sw = reinterpret_cast<Scalar*>(lds);
   const int lane = threadIdx.x & 63, prow = lane >> 3;
   const auto& col = pr.col;
   const auto& rp = pr.rp;
@@ -655,9 +686,9 @@ __device__ __forceinline__ void epilogue_pair(const Acc (&acc)[TM][TN], int64_t 
           uint2 out[Map::GPU];
 #pragma unroll
           for (int gg = 0; gg < Map::GPU; ++gg) {
-            const int32_t* w = sw + St::word(prow, 2 * (c + 4 * gg));
-            const int32_t gv[4] = {w[0], w[2], w[4], w[6]};
-            const int32_t uv[4] = {w[1], w[3], w[5], w[7]};
+            const Scalar* w = sw + St::word(prow, 2 * (c + 4 * gg));
+            const Scalar gv[4] = {w[0], w[2], w[4], w[6]};
+            const Scalar uv[4] = {w[1], w[3], w[5], w[7]};
             out[gg] = epi.apply(rp[i][q], col[h * Map::GPU + gg], gv, uv);
           }
           store_unit<Map::GPU>(epi, m, c0 + c, nv < Map::UNIT ? (int)nv : Map::UNIT, out);

@@ -90,4 +90,25 @@ pair_generic_kernel(int64_t M, int64_t NC, int64_t K, int64_t nbx, const int8_t*
   store_group(ep, m, col, 1, ep.pair4(m, col, gv, uv, 1));
 }
 
+// bf16 FFN pair fallback (MOSS bf16 FC1): fp32 sums in K order, each
+// product and sum rounded on its own.
+template <class Epi>
+__global__ void __launch_bounds__(256)
+pair_generic_bf16_kernel(int64_t M, int64_t NC, int64_t K, int64_t nbx, const uint16_t* a,
+                         int64_t lda, const uint16_t* g, const uint16_t* u, int64_t ldw, Epi epi) {
+  const int64_t bx = (int64_t)blockIdx.x % nbx, by = (int64_t)blockIdx.x / nbx;
+  const int64_t col = bx * 64 + (threadIdx.x & 63);
+  const int64_t m = by * 4 + (threadIdx.x >> 6);
+  if (m >= M || col >= NC) return;
+  const Epi ep = epi.prepare();
+  float ag = 0.0f, au = 0.0f;
+  for (int64_t k = 0; k < K; ++k) {
+    const float x = bf16_f32(a[m * lda + k]);
+    ag = ag + x * bf16_f32(g[col * ldw + k]);
+    au = au + x * bf16_f32(u[col * ldw + k]);
+  }
+  const float gv[4] = {ag, 0.0f, 0.0f, 0.0f}, uv[4] = {au, 0.0f, 0.0f, 0.0f};
+  store_group(ep, m, col, 1, ep.pair4(m, col, gv, uv, 1));
+}
+
 }  // namespace c4q

@@ -63,6 +63,22 @@ extern "C" int c4q_i8_gemm_nt_fused_cs(const int8_t* a, int64_t lda, const int8_
                                  as_stream(stream), what);
 }
 
+extern "C" int c4q_i8_gemm_nt_fused_cs_f16(const int8_t* a, int64_t lda, const int8_t* b,
+                                           int64_t ldb, uint16_t* d, int64_t ldd,
+                                           const float* row_scale, const float* col_scale,
+                                           const uint16_t* bias, int64_t M, int64_t N, int64_t K,
+                                           void* stream) {
+  const char* what = "c4q_i8_gemm_nt_fused_cs_f16";
+  int st = check_i8_args(a, lda, b, ldb, d, ldd, M, N, K, what);
+  if (st) return st;
+  C4Q_REQUIRE(M == 0 || N == 0 || (row_scale != nullptr && col_scale != nullptr), C4Q_ERR_ARG,
+              "%s: null row_scale/col_scale", what);
+  EpiRowColScaleF16 epi{{d, ldd, rows_vec16(d, ldd, 2)}, row_scale, col_scale, bias};
+  return run_gemm8<OpI8T, GenI8>(reinterpret_cast<const uint8_t*>(a), lda,
+                                 reinterpret_cast<const uint8_t*>(b), ldb, M, N, K, epi,
+                                 as_stream(stream), what);
+}
+
 extern "C" int c4q_i8_ffn_pair(const int8_t* a, int64_t lda, const int8_t* w_gate,
                                const int8_t* w_up, int64_t ldw, uint16_t* d, int64_t ldd,
                                const float* row_scale, const float* gate_scale,

@@ -5,13 +5,15 @@ modules (pybind11 functions taking tensors; a bad argument raises
 RuntimeError before any work is enqueued):
 
     i8_matmul2d_nt, i8_matmul2d_nt_fused, i8_matmul2d_nt_fused_cs,
+    i8_matmul2d_nt_fused_cs_half,
     i8_quant_rowwise                 (_patches/int8_ext/int8_gemm.mm:2626-2715)
     fp8fp8_matmul2d_nt               (_patches/fp8_ext/fp8_matmul2d.mm:229-265)
     w8a16_f32, w8a16_bias_bf16       (_patches/fp8s_ext/w8a16_gemm.mm:286-329)
 
 plus the whole-operation forms the patch layer uses: ``int_mm``
 (torch._int_mm), ``scaled_mm`` (torch._scaled_mm), ``fp8_quant_pertensor``,
-``fp8_dequant``, ``w8a16_linear`` and ``ffn_pair``.
+``fp8_dequant``, ``w8a16_linear``, ``ffn_pair`` and ``moss_bf16_pair`` (the
+bf16 FC1/SiTU pair of _patches/moss_bf16_ffn_pair.py:36-48).
 
 Every function enqueues on the current HIP stream of the tensors' device and
 returns without synchronizing. Outputs are allocated here with torch; the
@@ -158,6 +160,28 @@ def i8_matmul2d_nt_fused_cs(a_i8, b_i8, row_scale, col_scale, bias=None, split_t
     return d
 
 
+def i8_matmul2d_nt_fused_cs_half(a_i8, b_i8, row_scale, col_scale, bias=None):
+    """D[M,N] fp16 = half(f32(A@B^T) * (col_scale[n] * row_scale[m])) [then
+    half(D + bias[n])]; bias is converted to fp16 as the reference does
+    (_patches/int8_ext/int8_gemm.mm:1965-2010)."""
+    _req(a_i8.dim() == 2 and b_i8.dim() == 2, "a/b must be 2D")
+    _req(a_i8.size(1) == b_i8.size(1), "K mismatch: A[M,K], B[N,K]")
+    dev, lda, ldb = _i8_operands(a_i8, b_i8)
+    M, K = a_i8.shape
+    N = b_i8.size(0)
+    _dev(row_scale, col_scale, bias)
+    _vec(row_scale, M, torch.float32, "row_scale")
+    _vec(col_scale, N, torch.float32, "col_scale")
+    if bias is not None:
+        bias = _vec(bias.to(torch.float16).contiguous().reshape(-1), N, torch.float16, "bias")
+    d = torch.empty((M, N), dtype=torch.float16, device=dev)
+    with _on(dev):
+        _lib.call("c4q_i8_gemm_nt_fused_cs_f16", a_i8.data_ptr(), lda, b_i8.data_ptr(), ldb,
+                  d.data_ptr(), N, row_scale.data_ptr(), col_scale.data_ptr(),
+                  bias.data_ptr() if bias is not None else None, M, N, K, _stream(dev))
+    return d
+
+
 def i8_quant_rowwise(x):
     """x[M,K] bf16/f16 -> (q[M,K] int8, scales[M,1] fp32), bit-exact with
     comfy_kitchen quantize_int8_rowwise."""
@@ -199,6 +223,35 @@ def ffn_pair(q, w_gate, w_up, row_scale, gate_scale, up_scale, table_gate=None, 
                   table_gate.data_ptr() if table_gate is not None else None,
                   table_up.data_ptr() if table_up is not None else None, M, N, K, _stream(dev))
     return d
+
+
+def moss_bf16_pair(x, weight, tables):
+    """MOSS bf16 FC1 + SiTU, as the reference's project(x, weight, tables)
+    (_patches/moss_bf16_ffn_pair.py:36-48): weight [2F, K] bf16 splits into
+    hidden rows [0, F) and gate rows [F, 2F); out[..., F] bf16 =
+    bf16(f32(T_h[bf16(x@Wh^T)]) * f32(T_g[bf16(x@Wg^T)])) with fp32
+    accumulation; tables = (T_h, T_g), 65,536 bf16 entries each."""
+    _req(x.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16,
+         "x and weight must be bf16")
+    _req(weight.dim() == 2 and weight.size(0) % 2 == 0, "weight must be [2F, K]")
+    _req(x.size(-1) == weight.size(1), "K mismatch: x[..., K], weight[2F, K]")
+    th, tg = tables
+    dev = _dev(x, weight, th, tg)
+    for t in (th, tg):
+        _req(t.numel() == 65536 and t.element_size() == 2 and t.is_contiguous(),
+             "activation tables must be 65536 contiguous 16-bit entries")
+    lead = x.shape[:-1]
+    K = x.size(-1)
+    x2 = x.reshape(-1, K)
+    M = x2.size(0)
+    F = weight.size(0) // 2
+    ldw = _ld(weight, "weight")
+    wh, wg = weight[:F], weight[F:]
+    d = torch.empty((M, F), dtype=torch.bfloat16, device=dev)
+    with _on(dev):
+        _lib.call("c4q_bf16_ffn_pair", x2.data_ptr(), _ld(x2, "x"), wh.data_ptr(), wg.data_ptr(),
+                  ldw, d.data_ptr(), F, th.data_ptr(), tg.data_ptr(), M, F, K, _stream(dev))
+    return d.reshape(*lead, F)
 
 
 # ------------------------------------------------------------------- FP8 ---

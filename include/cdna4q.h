@@ -76,6 +76,17 @@ int c4q_i8_gemm_nt_fused_cs(const int8_t* a, int64_t lda, const int8_t* b, int64
                             const float* col_scale, const uint16_t* bias,
                             int64_t M, int64_t N, int64_t K, void* stream);
 
+/* fp16 variant: D[M,N] half = half(f32(A@B^T) * (col_scale[n] * row_scale[m]))
+ * [then half(f32(D) + f32(bias[n]))], bias: fp16 [N] or NULL.
+ * Replaces i8_matmul2d_nt_fused_cs_half (_patches/int8_ext/int8_gemm.mm:1965-2010,
+ * epilogue nax_frag_store_dequant_cs_half :1161-1183), called by the Wan and
+ * MiniMax-VAE INT8 projections (_patches/wan_fp16.py:40-42,
+ * _patches/minimax_vae_int8.py:71-73). */
+int c4q_i8_gemm_nt_fused_cs_f16(const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb,
+                                uint16_t* d, int64_t ldd, const float* row_scale,
+                                const float* col_scale, const uint16_t* bias,
+                                int64_t M, int64_t N, int64_t K, void* stream);
+
 /* Rowwise int8 activation quant of x[M,K] (bf16 or f16):
  * q[M,K] int8 and scales[M] fp32, bit-exact with comfy_kitchen
  * quantize_int8_rowwise. Replaces i8_quant_rowwise
@@ -140,6 +151,18 @@ int c4q_i8_ffn_pair(const int8_t* a, int64_t lda, const int8_t* w_gate, const in
                     const float* gate_scale, const float* up_scale,
                     const uint16_t* table_gate, const uint16_t* table_up,
                     int64_t M, int64_t N_out, int64_t K, void* stream);
+
+/* bf16 fused FC1/SiTU pair, bf16 out [M, N_out]:
+ *   h = bf16(f32(A@Wh^T)),  g = bf16(f32(A@Wg^T))   (fp32 accumulation)
+ *   D = bf16(f32(T_h[h]) * f32(T_g[g]))              (NULL table = identity)
+ * A [M,K] bf16; Wh, Wg [N_out, K] bf16 with row stride ldw: the hidden and
+ * gate halves of one [2F, K] weight; T_h / T_g the SiTU tables (65,536 bf16).
+ * Replaces moss_64_128_2_4_0 (_patches/moss_bf16_ffn_pair.metal:282-304)
+ * behind project() (_patches/moss_bf16_ffn_pair.py:36-48). */
+int c4q_bf16_ffn_pair(const uint16_t* a, int64_t lda, const uint16_t* w_hidden,
+                      const uint16_t* w_gate, int64_t ldw, uint16_t* d, int64_t ldd,
+                      const uint16_t* table_hidden, const uint16_t* table_gate,
+                      int64_t M, int64_t N_out, int64_t K, void* stream);
 
 #ifdef __cplusplus
 }

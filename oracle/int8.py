@@ -61,6 +61,20 @@ def epilogue_rowcolscale(c, row_scale, col_scale, bias_bits=None):
     return d
 
 
+def epilogue_rowcolscale_half(c, row_scale, col_scale, bias_f16_bits=None):
+    """fp16 per-channel epilogue: s = col_scale[n] * row_scale[m] (f32),
+    D = half(f32(C) * s), then with a bias D = half(f32(D) + f32(bias[n])),
+    bias in fp16. Half rounding is RNE and overflows to +-inf, as Metal's
+    half() conversion. Reference ``_patches/int8_ext/int8_gemm.mm:1161-1183``
+    (entry ``i8_matmul2d_nt_fused_cs_half`` ``:1965-2010``)."""
+    cf = np.asarray(c, dtype=np.int32).astype(F32)
+    s = np.asarray(col_scale, dtype=F32)[None, :] * np.asarray(row_scale, dtype=F32)[:, None]
+    d = f32_to_f16_bits(cf * s)
+    if bias_f16_bits is not None:
+        d = f32_to_f16_bits(f16_bits_to_f32(d) + f16_bits_to_f32(bias_f16_bits)[None, :])
+    return d
+
+
 BF16_TINY = F32(2.0 ** -126)   # torch.finfo(torch.bfloat16).tiny
 F16_TINY = F32(2.0 ** -14)     # torch.finfo(torch.float16).tiny
 

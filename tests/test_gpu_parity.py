@@ -105,6 +105,118 @@ def test_i8_fused_cs_exact(dev, M, K, N, bias):
     assert_bits_equal(bits16(d), ref, f"fused_cs {M}x{K}x{N}")
 
 
+# fp16-output per-channel epilogue (the Wan / MiniMax-VAE INT8 projections)
+FUSED_HALF_CASES = [(1, 64, 16, True), (300, 1040, 520, True), (257, 512, 384, False),
+                    (1024, 3072, 3072, True)]
+
+
+@pytest.mark.parametrize("M,K,N,bias", FUSED_HALF_CASES)
+def test_i8_fused_cs_half_exact(dev, M, K, N, bias):
+    """Column scales spread the results from fp16 subnormals to overflow
+    (inf); zero scales in row 0 / column 0."""
+    g = gen(41 + M + N)
+    a, b = _randint8((M, K), g), _randint8((N, K), g)
+    rs = torch.rand(M, generator=g) * 0.01
+    cs = torch.rand(N, generator=g) * 0.02 * torch.logspace(-5, 2, N)
+    rs[0] = 0.0
+    cs[0] = 0.0
+    bb = (torch.randn(N, generator=g) * 4).to(torch.float16) if bias else None
+    d = ops.i8_matmul2d_nt_fused_cs_half(a.to(dev), b.to(dev), rs.to(dev), cs.to(dev),
+                                         bb.to(dev) if bias else None)
+    assert d.dtype == torch.float16 and d.shape == (M, N)
+    ref = oi.epilogue_rowcolscale_half(oi.i8_matmul2d_nt(a.numpy(), b.numpy()), rs.numpy(),
+                                       cs.numpy(), bits16(bb) if bias else None)
+    assert_bits_equal(bits16(d), ref, f"fused_cs_half {M}x{K}x{N}")
+
+
+def test_i8_fused_cs_half_strided_generic(dev):
+    """Row strides that are not multiples of 16 take the generic kernel."""
+    g = gen(43)
+    M, K, N = 70, 200, 90
+    a = _randint8((M, K + 3), g)[:, :K]
+    b = _randint8((N, K + 5), g)[:, :K]
+    rs = torch.rand(M, generator=g) * 0.01
+    cs = torch.rand(N, generator=g) * 0.02
+    bb = torch.randn(N, generator=g).to(torch.float16)
+    d = ops.i8_matmul2d_nt_fused_cs_half(a.to(dev), b.to(dev), rs.to(dev), cs.to(dev), bb.to(dev))
+    ref = oi.epilogue_rowcolscale_half(oi.i8_matmul2d_nt(a.numpy(), b.numpy()), rs.numpy(),
+                                       cs.numpy(), bits16(bb))
+    assert_bits_equal(bits16(d), ref, "fused_cs_half generic")
+
+
+def test_f16_outputs_round_f32_results_once(dev):
+    """fp16 outputs of _scaled_mm and W8A16 over exact integer sums must
+    match the oracle bit for bit: their epilogues multiply and add in f32 and
+    round the f32 result to half. A conversion fused with the last f32
+    operation (v_fma_mixlo_f16) would round the exact value instead, which
+    gives another half wherever the f32 result is a half tie."""
+    g = gen(61)
+    M, K, N = 300, 512, 520
+    af = torch.randint(-8, 9, (M, K), generator=g).float().to(torch.float8_e4m3fn)   # small integers: exact e4m3
+    wf = torch.randint(-8, 9, (N, K), generator=g).float().to(torch.float8_e4m3fn)
+    sa = torch.rand(M, 1, generator=g) * 0.01 + 0.001
+    sb = torch.rand(1, N, generator=g) * 0.01 + 0.001
+    bias = (torch.randn(N, generator=g) * 2).to(torch.float16)
+    o = ops.scaled_mm(af.to(dev), wf.to(dev).t(), out_dtype=torch.float16, scale_a=sa.to(dev),
+                      scale_b=sb.to(dev), bias=bias.to(dev))
+    ref = of.scaled_mm(u8(af), u8(wf), sa.numpy(), sb.numpy(), bits16(bias), "f16",
+                       out_dtype="f16")
+    assert_bits_equal(bits16(o), ref, "scaled_mm f16 out")
+    x = (torch.randint(-8, 9, (M, K), generator=g) * 0.125).to(torch.float16)
+    bw = (torch.randn(N, generator=g) * 0.3).to(torch.float16)
+    y = ops.w8a16_linear(x.to(dev), wf.to(dev), None, bw.to(dev))
+    ref = of.w8a16_linear(bits16(x), u8(wf), None, bits16(bw), "f16", x_dtype="f16",
+                          out_dtype="f16")
+    assert_bits_equal(bits16(y), ref, "w8a16 f16 out")
+
+
+# MOSS bf16 FC1/SiTU pair
+def _moss_tables(dev):
+    return tuple(torch.from_numpy(t.view(np.int16)).to(dev) for t in oact.situ_tables())
+
+
+@pytest.mark.parametrize("M,K,F", [(129, 3072, 8192), (300, 1040, 520), (1, 64, 64),
+                                   (77, 136, 100)])
+def test_moss_bf16_pair_integer_exact(dev, M, K, F):
+    """Quarter-integer operands: every fp32 sum is exact in any order, so the
+    kernel must equal the oracle bit for bit (first case: the reference's
+    MOSS weight [16384, 3072])."""
+    g = gen(51 + M + F)
+    x = (torch.randint(-6, 7, (M, K), generator=g) * 0.25).to(torch.bfloat16)
+    w = (torch.randint(-6, 7, (2 * F, K), generator=g) * 0.25).to(torch.bfloat16)
+    out = ops.moss_bf16_pair(x.to(dev), w.to(dev), _moss_tables(dev))
+    assert out.shape == (M, F) and out.dtype == torch.bfloat16
+    ref = op.moss_bf16_pair(bits16(x), bits16(w), *oact.situ_tables())
+    assert_bits_equal(bits16(out), ref, f"moss bf16 pair {M}x{K}x{F}")
+
+
+def test_moss_bf16_pair_random(dev):
+    g = gen(55)
+    M, K, F = 512, 3072, 1024
+    x = torch.randn(1, M, K, generator=g).to(torch.bfloat16)
+    w = (0.02 * torch.randn(2 * F, K, generator=g)).to(torch.bfloat16)
+    out = ops.moss_bf16_pair(x.to(dev), w.to(dev), _moss_tables(dev))
+    assert out.shape == (1, M, F)
+    ref = op.moss_bf16_pair(bits16(x[0]), bits16(w), *oact.situ_tables())
+    assert_close(bf16_to_f32(bits16(out[0])), bf16_to_f32(ref), "moss bf16 pair random")
+
+
+def test_moss_bf16_pair_generic_and_split_k(dev, monkeypatch):
+    """A row stride that is not a multiple of 8 takes the generic kernel; the
+    forced split-K tile runs the same pair on 64x64 pieces."""
+    g = gen(57)
+    M, K, F = 100, 264, 96
+    x = (torch.randint(-6, 7, (M, K + 3), generator=g) * 0.25).to(torch.bfloat16)[:, :K]
+    w = (torch.randint(-6, 7, (2 * F, K), generator=g) * 0.25).to(torch.bfloat16)
+    ref = op.moss_bf16_pair(bits16(x), bits16(w), *oact.situ_tables())
+    out = ops.moss_bf16_pair(x.to(dev), w.to(dev), _moss_tables(dev))
+    assert_bits_equal(bits16(out), ref, "moss bf16 pair generic")
+    monkeypatch.setenv("C4Q_TILE", "7")
+    xc = x.contiguous()
+    out = ops.moss_bf16_pair(xc.to(dev), w.to(dev), _moss_tables(dev))
+    assert_bits_equal(bits16(out), ref, "moss bf16 pair split-K")
+
+
 def test_c1_golden_digest_full_size(dev):
     """BASELINE C1 at full size (seed 1): the kernel's INT32 product and
     per-channel bf16 epilogue hash to the digests written from torch._int_mm
@@ -410,7 +522,7 @@ def test_moss_pair_exact(dev):
 
 # ---------------------------------------------------- every tile variant ---
 
-@pytest.mark.parametrize("tile", [str(t) for t in range(7)])
+@pytest.mark.parametrize("tile", [str(t) for t in range(8)])
 def test_every_tile_variant(dev, monkeypatch, tile):
     """Force each MFMA tile variant (C4Q_TILE) on ragged shapes: INT8 fused
     epilogue and pair bit-exact, fp8 / W8A16 within tolerance."""
@@ -427,6 +539,15 @@ def test_every_tile_variant(dev, monkeypatch, tile):
     d = ops.i8_matmul2d_nt_fused_cs(a.to(dev), b.to(dev), rs.to(dev), cs.to(dev), bb.to(dev))
     assert_bits_equal(bits16(d), oi.epilogue_rowcolscale(ref_c, rs.numpy(), cs.numpy(), bits16(bb)),
                       f"tile {tile} fused_cs")
+    bh = bb.to(torch.float16)
+    h = ops.i8_matmul2d_nt_fused_cs_half(a.to(dev), b.to(dev), rs.to(dev), cs.to(dev), bh.to(dev))
+    assert_bits_equal(bits16(h), oi.epilogue_rowcolscale_half(ref_c, rs.numpy(), cs.numpy(),
+                                                              bits16(bh)), f"tile {tile} fused_cs_half")
+    xq = (torch.randint(-6, 7, (M, K), generator=g) * 0.25).to(torch.bfloat16)
+    wq = (torch.randint(-6, 7, (2 * N, K), generator=g) * 0.25).to(torch.bfloat16)
+    mp = ops.moss_bf16_pair(xq.to(dev), wq.to(dev), _moss_tables(dev))
+    assert_bits_equal(bits16(mp), op.moss_bf16_pair(bits16(xq), bits16(wq), *oact.situ_tables()),
+                      f"tile {tile} moss bf16 pair")
     wu = _randint8((N, K), g)
     us = torch.rand(N, generator=g) * 0.02
     silu = torch.from_numpy(oact.silu_table().view(np.int16))

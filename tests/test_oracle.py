@@ -160,6 +160,26 @@ def test_epilogue_rowcolscale_order_matches_torch_eager():
     assert np.array_equal(got, tbits(wb))
 
 
+def test_epilogue_rowcolscale_half_matches_torch_eager():
+    c, rs, cs, _ = _epi_case(21, 256, 512)
+    cs = cs * torch.logspace(-5, 3, 512)          # results from fp16 subnormals to overflow
+    bias = (torch.randn(512, generator=torch.Generator().manual_seed(22)) * 4).to(torch.float16)
+    want = (c.float() * (cs[None, :] * rs[:, None])).to(torch.float16)
+    got = oi.epilogue_rowcolscale_half(c.numpy(), rs.numpy(), cs.numpy())
+    assert np.array_equal(got, tbits(want))
+    wf = want.float()
+    assert torch.isinf(wf).any() and ((wf != 0) & (wf.abs() < 2.0 ** -14)).any()
+    wb = (want.float() + bias.float()).to(torch.float16)      # second rounding (bias)
+    got_b = oi.epilogue_rowcolscale_half(c.numpy(), rs.numpy(), cs.numpy(), tbits(bias))
+    assert np.array_equal(got_b, tbits(wb))
+    # one rounding instead of two, and a bf16 first rounding, each differ somewhere
+    one = (c.float() * (cs[None, :] * rs[:, None]) + bias.float()).to(torch.float16)
+    assert not np.array_equal(tbits(one), tbits(wb))
+    via_bf16 = ((c.float() * (cs[None, :] * rs[:, None])).to(torch.bfloat16).float()
+                + bias.float()).to(torch.float16)
+    assert not np.array_equal(tbits(via_bf16), tbits(wb))
+
+
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
 def test_quant_rowwise_golden_edges(dt):
     g = np.load(GOLD / "quant_rowwise.npz")
@@ -318,6 +338,44 @@ def test_moss_pair_is_the_unfused_torch_chain():
     th, tg = oact.situ_tables()
     got = op.moss_pair(q.numpy(), w.numpy(), rs.numpy(), cs.numpy(), th, tg)
     assert np.array_equal(got, tbits(want))
+
+
+def _situ(h, g):
+    return (25.0 * torch.tanh(h / 25.0)) * (4.0 * torch.tanh(g / 4.0) * torch.sigmoid(g))
+
+
+def test_moss_bf16_pair_is_the_unfused_torch_chain():
+    """Integer-valued bf16 operands (multiples of 1/4): every fp32 sum is
+    exact in any order, so torch's CPU bf16 linear is exact and the chain
+    linear -> SiTU (bf16 ops) must match bit for bit."""
+    g = torch.Generator().manual_seed(31)
+    M, K, F_ = 40, 384, 72
+    x = (torch.randint(-6, 7, (M, K), generator=g) * 0.25).to(torch.bfloat16)
+    w = (torch.randint(-6, 7, (2 * F_, K), generator=g) * 0.25).to(torch.bfloat16)
+    wh, wg = w.chunk(2, dim=0)
+    want = _situ(F.linear(x, wh), F.linear(x, wg))
+    th, tg = oact.situ_tables()
+    got = op.moss_bf16_pair(tbits(x), tbits(w), th, tg)
+    assert np.array_equal(got, tbits(want))
+    # swapped halves or swapped tables (plausible mistakes) differ
+    assert not np.array_equal(op.moss_bf16_pair(tbits(x), tbits(torch.cat([wg, wh])), th, tg), got)
+    assert not np.array_equal(op.moss_bf16_pair(tbits(x), tbits(w), tg, th), got)
+
+
+def test_moss_bf16_pair_random_within_one_rounding_of_torch():
+    """Random operands: torch's fp32 summation order differs from the exact
+    sum, so h / g may differ by one bf16 ulp; the outputs then agree to the
+    slope of SiTU times that ulp."""
+    g = torch.Generator().manual_seed(32)
+    x = torch.randn(32, 512, generator=g).to(torch.bfloat16)
+    w = (0.05 * torch.randn(160, 512, generator=g)).to(torch.bfloat16)
+    wh, wg = w.chunk(2, dim=0)
+    want = bf16_bits_to_f32(tbits(_situ(F.linear(x, wh), F.linear(x, wg))))
+    th, tg = oact.situ_tables()
+    got = bf16_bits_to_f32(op.moss_bf16_pair(tbits(x), tbits(w), th, tg))
+    scale = np.abs(want).max()
+    assert (np.abs(got - want) <= 2.0 ** -6 * np.abs(want) + 2.0 ** -9 * scale).all()
+    assert (got == want).mean() > 0.9
 
 
 def test_cpu_baseline_paths_compute_the_oracle_results():
