@@ -10,7 +10,8 @@ TFLOP/s (2*M*K*N per linear). ``roofline`` covers the dominant kernel of
 that step (the QKV W8A16 GEMM: one launch of whole rounds of 256x256 tiles
 plus one launch of the leftover tiles as split-K 64x64 pieces), timed with HIP
 events around each QKV call inside the timed region. ``per_config`` adds C1, C3, C4 and C5
-measured in the same process; ``cpu_baseline`` times the reference's
+measured in the same process, plus MOSS_BF16 and WAN_FP16 (the bf16 FC1/SiTU
+pair and the fp16-output INT8 epilogue, not BASELINE configs); ``cpu_baseline`` times the reference's
 PyTorch CPU path for C2 (kitchen dequant + bf16 F.linear) on a bounded row
 sample on this host's cores.
 
@@ -249,6 +250,45 @@ def bench_c4(torch, ops, dev, steps, warmup):
             "frac_int8_peak": ops_ / kern / 1e12 / PEAK["int8"], "act_quant_ms": qwall * 1e3}
 
 
+# ------------------------------------------------- widened rows (extra) ---
+# Not BASELINE configs: the MOSS bf16 FC1/SiTU pair at the reference's own
+# gate shape (x [1, 4096, 3072] bf16, weight [16384, 3072] bf16) and the
+# fp16-output INT8 epilogue on the Wan 14B projection weights (the
+# reference's shape list), over 9216 token rows.
+
+def bench_moss_bf16(torch, ops, dev, steps, warmup):
+    M, K, F2 = 4096, 3072, 16384
+    g = torch.Generator(device=dev).manual_seed(6)
+    x = torch.randn(1, M, K, generator=g, device=dev).to(torch.bfloat16)
+    w = (0.02 * torch.randn(F2, K, generator=g, device=dev)).to(torch.bfloat16)
+    tabs = ops.situ_tables(dev)
+    wall, kern = Timer(torch).run(lambda p: marked(p, lambda: ops.moss_bf16_pair(x, w, tabs)),
+                                  steps, warmup)
+    fl = 2.0 * M * F2 * K
+    return {"shape": [M, K, F2], "pair_ms": kern * 1e3, "tflops": fl / kern / 1e12,
+            "frac_bf16_peak": fl / kern / 1e12 / PEAK["bf16"]}
+
+
+def bench_wan_fp16(torch, ops, dev, steps, warmup):
+    M = 9216
+    g = torch.Generator(device=dev).manual_seed(7)
+    res = {}
+    for (N, K) in ((5120, 5120), (13824, 5120), (5120, 13824)):
+        x = torch.randint(-127, 128, (M, K), generator=g, device=dev, dtype=torch.int8)
+        w = torch.randint(-127, 128, (N, K), generator=g, device=dev, dtype=torch.int8)
+        rs = 0.005 + 0.015 * torch.rand(M, generator=g, device=dev)
+        cs = 0.0005 + 0.0015 * torch.rand(N, generator=g, device=dev)
+        b = torch.randn(N, generator=g, device=dev).to(torch.float16)
+        _, kern = Timer(torch).run(
+            lambda p: marked(p, lambda: ops.i8_matmul2d_nt_fused_cs_half(x, w, rs, cs, b)),
+            max(5, steps // 2), max(2, warmup // 2))
+        o = 2.0 * M * N * K
+        res[f"{N}x{K}"] = {"shape": [M, K, N], "kernel_ms": kern * 1e3, "tops": o / kern / 1e12,
+                           "frac_int8_peak": o / kern / 1e12 / PEAK["int8"]}
+        del x, w
+    return res
+
+
 # ----------------------------------------------------------------- C5 ---
 
 def bench_c5(torch, ops, dev, steps, warmup):
@@ -391,8 +431,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--only", default="C1,C2,C3,C4,C5",
-                    help="comma list of configs to run (C2 is always run)")
+    ap.add_argument("--only", default="C1,C2,C3,C4,C5,MOSS_BF16,WAN_FP16",
+                    help="comma list of configs to run (C2 is always run); MOSS_BF16 and "
+                         "WAN_FP16 time the widened rows (not BASELINE configs)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--pmc-target", action="store_true",
                     help="run the copy calibration and the C2 QKV kernel for rocprofv3 --pmc")
@@ -420,7 +461,8 @@ def main():
     log("C2 (headline) ...")
     c2 = bench_c2(torch, ops, dev, args.steps, args.warmup)
     torch.cuda.empty_cache()
-    for name, fn in (("C1", bench_c1), ("C3", bench_c3), ("C4", bench_c4), ("C5", bench_c5)):
+    for name, fn in (("C1", bench_c1), ("C3", bench_c3), ("C4", bench_c4), ("C5", bench_c5),
+                     ("MOSS_BF16", bench_moss_bf16), ("WAN_FP16", bench_wan_fp16)):
         if name in only:
             log(f"{name} ...")
             per[name] = fn(torch, ops, dev, args.steps, args.warmup)

@@ -9,17 +9,19 @@ reference patch:
     linear_fp8_w8a16  standard-fp8 Linear forward    (_patches/linear_fp8_w8a16.py)
     krea2_ffn_pair    Krea2 SwiGLU gate/up pair      (_patches/krea2_ffn_pair.py)
     moss_ffn          MOSS FC1 + SiTU pair           (_patches/moss_ffn_mps.py)
+    moss_bf16_ffn_pair  MOSS bf16 FC1 + SiTU pair    (_patches/moss_bf16_ffn_pair.py)
 
 ``install_all()`` installs every patch whose host (a ROCm device, ComfyUI for
 the model seams) is present and returns the names installed. Each module also
 honours its own ``C4Q_<NAME>=0`` switch.
 """
-from . import int8_linear, int_mm, krea2_ffn_pair, linear_fp8_w8a16, moss_ffn, scaled_mm_fp8
+from . import (int8_linear, int_mm, krea2_ffn_pair, linear_fp8_w8a16, moss_bf16_ffn_pair, moss_ffn,
+               scaled_mm_fp8)
 from . import _common
 
 _ALL = (("int_mm", int_mm), ("scaled_mm_fp8", scaled_mm_fp8), ("int8_linear", int8_linear),
         ("linear_fp8_w8a16", linear_fp8_w8a16), ("krea2_ffn_pair", krea2_ffn_pair),
-        ("moss_ffn", moss_ffn))
+        ("moss_ffn", moss_ffn), ("moss_bf16_ffn_pair", moss_bf16_ffn_pair))
 
 
 def install_all():

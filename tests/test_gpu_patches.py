@@ -149,3 +149,20 @@ def test_moss_project_exact(dev):
     out = moss_ffn.project(q.to(dev), rs.to(dev), w.to(dev), cs.to(dev), tabs)
     ref = op.moss_pair(q.numpy(), w.numpy(), rs.numpy(), cs.numpy(), th, tg)
     assert_bits_equal(bits16(out), ref, "moss project")
+
+
+def test_moss_bf16_project_exact(dev):
+    """The reference's MOSS shape (x [1, 4096, 3072], weight [16384, 3072])
+    through the patch's gate and project, quarter-integer operands (exact
+    fp32 sums in any order): bit-exact against the oracle."""
+    from cdna4q.patches import moss_bf16_ffn_pair as mb
+    g = gen(29)
+    x = (torch.randint(-6, 7, (1, 4096, 3072), generator=g) * 0.25).to(torch.bfloat16)
+    w = (torch.randint(-6, 7, (16384, 3072), generator=g) * 0.25).to(torch.bfloat16)
+    xd, wd = x.to(dev), w.to(dev)
+    assert mb.eligible(xd, wd)
+    out = mb.project(xd, wd)
+    assert out.shape == (1, 4096, 8192)
+    rows = slice(0, 4096, 37)                   # the oracle on a row sample (seconds, not minutes)
+    ref = op.moss_bf16_pair(bits16(x[0, rows]), bits16(w), *oact.situ_tables())
+    assert_bits_equal(bits16(out[0, rows]), ref, "moss bf16 project")

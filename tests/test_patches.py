@@ -286,6 +286,27 @@ def test_moss_project_splits_hidden_and_gate_rows(monkeypatch):
         moss_ffn.project(q, torch.ones(4), _i8((7, 16), 3), torch.ones(7), (th, tg))
 
 
+def test_moss_bf16_project_and_gate(monkeypatch):
+    from cdna4q.patches import moss_bf16_ffn_pair as mb
+    fake = Rec(lambda *a: "pair")
+    monkeypatch.setattr(ops, "moss_bf16_pair", fake)
+    x = torch.zeros(1, 8, 16, dtype=torch.bfloat16)
+    w = torch.zeros(12, 16, dtype=torch.bfloat16)
+    tabs = (torch.zeros(65536, dtype=torch.int16), torch.ones(65536, dtype=torch.int16))
+    assert mb.project(x, w, tabs) == "pair"
+    a = fake.calls[0][0]
+    assert a[0] is x and a[1] is w and a[2] is tabs
+    with pytest.raises(_lib.C4QError):
+        mb.project(x, torch.zeros(7, 16, dtype=torch.bfloat16), tabs)
+    # the reference's gate: [1, 4096..6656, 3072] bf16 activations, [16384, 3072] bf16 weight
+    xs = torch.empty(1, 4096, 3072, dtype=torch.bfloat16)
+    ws = torch.empty(16384, 3072, dtype=torch.bfloat16)
+    assert not mb.eligible(xs, ws)                                  # CPU tensors
+    assert not mb.eligible(xs[:, :10], ws)
+    assert not mb.eligible(torch.empty(1, 4096, 3072), ws)
+    assert mb.install() is False
+
+
 def test_krea2_candidate_gate(cpu_gate, monkeypatch):
     monkeypatch.setattr(krea2_ffn_pair, "project", Rec(lambda x, g, u: torch.zeros(2, 8)))
     down = Rec(lambda h: "down(pair)")
