@@ -54,6 +54,89 @@ quant_rowwise_kernel(const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, flo
   }
 }
 
+// Fused head merge + ConvRot + rowwise quant (reference
+// i8_merge_rot_quant_bf16, _patches/int8_ext/int8_gemm.mm:1429-1507): x
+// [B, H, S, D] bf16 contiguous; output row (b, s) of the merged [B*S, H*D]
+// matrix, element i = h*D + d. One workgroup per output row. With ROTATE,
+// every 256-element group is transformed by the radix-4 Walsh-Hadamard
+// butterflies at strides 1, 4, 16, 64 (row `digit` of
+// H4 = [[1,1,1,-1],[1,1,-1,1],[1,-1,1,1],[-1,1,1,1]] applied to the values at
+// base + k*stride, each sum in fp32 in the written order), scaled by 2^-4 and
+// rounded to bf16. Wave w takes groups w, w + 4, ...: lane l holds group
+// elements l + 64 j (j = 0..3), so the stride-64 stage is lane-local and the
+// other three stages go through a wave-private LDS row (no workgroup
+// barrier). The rotated row stays in LDS for the quant pass, which is the
+// rowwise arithmetic above.
+__device__ __forceinline__ float h4_row(int digit, float a0, float a1, float a2, float a3) {
+  if (digit == 0) return a0 + a1 + a2 - a3;
+  if (digit == 1) return a0 + a1 - a2 + a3;
+  if (digit == 2) return a0 - a1 + a2 + a3;
+  return -a0 + a1 + a2 + a3;
+}
+
+template <bool ROTATE>
+__global__ void __launch_bounds__(256)
+merge_rot_quant_kernel(const uint16_t* x, int64_t H, int64_t S, int64_t D, int8_t* q,
+                       float* scales) {
+  extern __shared__ uint16_t rot[];            // the row's H*D rotated bf16 values
+  __shared__ float work[4][256];
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const int64_t b = row / S, s = row - b * S;
+  const int64_t K = H * D;
+  const int groups = (int)(K >> 8);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  float* w = work[wave];
+  float mx = 0.0f;
+  for (int g = wave; g < groups; g += 4) {
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t i = (int64_t)g * 256 + lane + 64 * j;
+      const int64_t h = i / D, d = i - h * D;
+      v[j] = bf16_f32(x[((b * H + h) * S + s) * D + d]);
+    }
+    if constexpr (ROTATE) {
+#pragma unroll
+      for (int stride = 1; stride <= 16; stride *= 4) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) w[lane + 64 * j] = v[j];
+        lds_fence_wave();
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int idx = lane + 64 * j;
+          const int digit = (idx / stride) & 3;
+          const int base = idx - digit * stride;
+          v[j] = h4_row(digit, w[base], w[base + stride], w[base + 2 * stride], w[base + 3 * stride]);
+        }
+        lds_fence_wave();
+      }
+      // stride 64: the four values of the group are this lane's v[0..3],
+      // and element l + 64 j has digit j
+      const float a0 = v[0], a1 = v[1], a2 = v[2], a3 = v[3];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] = bf16_f32(bf16_rte(h4_row(j, a0, a1, a2, a3) * 0.0625f));
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      rot[g * 256 + lane + 64 * j] = (uint16_t)(f32_bits(v[j]) >> 16);   // v[j] is a bf16 value
+      mx = fmaxf(mx, fabsf(v[j]));
+    }
+  }
+  const float amax = block_max256(mx, red);    // also orders the rot writes before the reads
+  const float scale = fmaxf(amax / 127.0f, 1e-30f);
+  if (threadIdx.x == 0) scales[row] = scale;
+  float sc = round_half(scale, true);
+  if (sc == 0.0f) sc = 1.1754943508222875e-38f;
+  int8_t* qr = q + row * K;
+  for (int64_t i = threadIdx.x; i < K; i += 256) {
+    float r = round_half(bf16_f32(rot[i]) / sc, true);
+    r = rintf(r);
+    r = fminf(fmaxf(r, -128.0f), 127.0f);
+    qr[i] = (int8_t)(int)r;
+  }
+}
+
 __global__ void fill_zero_kernel(float* p) { p[0] = 0.0f; }
 
 // amax of |x| over n elements into *amax (bits of a non-negative float
@@ -147,6 +230,33 @@ extern "C" int c4q_i8_quant_rowwise(const void* x, int x_dtype, int64_t ldx, int
   else
     hipLaunchKernelGGL(quant_rowwise_kernel<false>, dim3((unsigned)M), dim3(256), 0, s, xs, ldx, q,
                        ldq, scales, K);
+  return check_launch(what);
+}
+
+extern "C" int c4q_i8_merge_rot_quant(const uint16_t* x, int64_t B, int64_t H, int64_t S,
+                                      int64_t D, int rotate, int8_t* q, float* scales,
+                                      void* stream) {
+  const char* what = "c4q_i8_merge_rot_quant";
+  C4Q_REQUIRE(B >= 0 && H >= 1 && S >= 0 && D > 0 && D <= 256, C4Q_ERR_SHAPE,
+              "%s: need B, S >= 0, H >= 1, 0 < D <= 256 (B=%lld H=%lld S=%lld D=%lld)", what,
+              (long long)B, (long long)H, (long long)S, (long long)D);
+  const int64_t K = H * D;
+  C4Q_REQUIRE(K % 256 == 0, C4Q_ERR_SHAPE, "%s: merged width H*D=%lld must tile 256-element groups",
+              what, (long long)K);
+  C4Q_REQUIRE(K * 2 <= 30 * 1024, C4Q_ERR_SHAPE, "%s: H*D=%lld too large (at most 15360)", what,
+              (long long)K);
+  const int64_t M = B * S;
+  if (M == 0) return C4Q_OK;
+  C4Q_REQUIRE(M < (1ll << 31), C4Q_ERR_SHAPE, "%s: too many rows", what);
+  C4Q_REQUIRE(x && q && scales, C4Q_ERR_ARG, "%s: null pointer", what);
+  hipStream_t s = as_stream(stream);
+  const size_t lds = (size_t)K * 2;
+  if (rotate)
+    hipLaunchKernelGGL(merge_rot_quant_kernel<true>, dim3((unsigned)M), dim3(256), lds, s, x, H, S,
+                       D, q, scales);
+  else
+    hipLaunchKernelGGL(merge_rot_quant_kernel<false>, dim3((unsigned)M), dim3(256), lds, s, x, H, S,
+                       D, q, scales);
   return check_launch(what);
 }
 

@@ -6,7 +6,7 @@ RuntimeError before any work is enqueued):
 
     i8_matmul2d_nt, i8_matmul2d_nt_fused, i8_matmul2d_nt_fused_cs,
     i8_matmul2d_nt_fused_cs_half,
-    i8_quant_rowwise                 (_patches/int8_ext/int8_gemm.mm:2626-2715)
+    i8_quant_rowwise, i8_merge_rot_quant (_patches/int8_ext/int8_gemm.mm:2626-2715)
     fp8fp8_matmul2d_nt               (_patches/fp8_ext/fp8_matmul2d.mm:229-265)
     w8a16_f32, w8a16_bias_bf16       (_patches/fp8s_ext/w8a16_gemm.mm:286-329)
 
@@ -180,6 +180,27 @@ def i8_matmul2d_nt_fused_cs_half(a_i8, b_i8, row_scale, col_scale, bias=None):
                   d.data_ptr(), N, row_scale.data_ptr(), col_scale.data_ptr(),
                   bias.data_ptr() if bias is not None else None, M, N, K, _stream(dev))
     return d
+
+
+def i8_merge_rot_quant(x, rotate=True):
+    """x [B,H,S,D] bf16 (attention layout) -> (q [B*S, H*D] int8,
+    scales [B*S, 1] fp32): head merge, ConvRot rotation of every 256-element
+    group (rotate=True) and rowwise int8 quant in one pass
+    (_patches/int8_ext/int8_gemm.mm:2545-2585)."""
+    _req(x.dim() == 4, "x must be [B,H,S,D]")
+    _req(x.dtype == torch.bfloat16, "x must be bf16")
+    _req(x.is_contiguous(), "x must be contiguous")
+    dev = _dev(x)
+    B, H, S, D = x.shape
+    K = H * D
+    _req(0 < D <= 256 and K % 256 == 0, "merged width must tile 256-element convrot groups")
+    _req(H >= 1 and K * 2 <= 30 * 1024, "H*D too large for threadgroup memory")
+    q = torch.empty((B * S, K), dtype=torch.int8, device=dev)
+    scales = torch.empty((B * S, 1), dtype=torch.float32, device=dev)
+    with _on(dev):
+        _lib.call("c4q_i8_merge_rot_quant", x.data_ptr(), B, H, S, D, 1 if rotate else 0,
+                  q.data_ptr(), scales.data_ptr(), _stream(dev))
+    return q, scales
 
 
 def i8_quant_rowwise(x):

@@ -94,6 +94,18 @@ int c4q_i8_gemm_nt_fused_cs_f16(const int8_t* a, int64_t lda, const int8_t* b, i
 int c4q_i8_quant_rowwise(const void* x, int x_dtype, int64_t ldx, int8_t* q, int64_t ldq,
                          float* scales, int64_t M, int64_t K, void* stream);
 
+/* Fused attention head merge + ConvRot rotation + rowwise int8 quant:
+ * x [B,H,S,D] bf16 contiguous -> q [B*S, H*D] int8 (row (b,s), column h*D+d)
+ * and scales [B*S] fp32. rotate != 0: each 256-element group of a row is
+ * rotated by the radix-4 Walsh-Hadamard butterflies of the reference kernel,
+ * times 2^-4, rounded to bf16; rotate == 0: gather only. The quant is the
+ * c4q_i8_quant_rowwise arithmetic. Needs 0 < D <= 256, H*D a multiple of 256
+ * and at most 15360. Replaces i8_merge_rot_quant
+ * (_patches/int8_ext/int8_gemm.mm:2545-2585, kernel :1429-1507), called by
+ * int8_o_proj_prequant (_patches/int8_linear_kernel_mps.py:436-535). */
+int c4q_i8_merge_rot_quant(const uint16_t* x, int64_t B, int64_t H, int64_t S, int64_t D,
+                           int rotate, int8_t* q, float* scales, void* stream);
+
 /* torch._scaled_mm fp8 route: D[M,N] = out_dtype(((f32(A@B^T) * scale_a)
  * * scale_b) * scale_result + f32(bias[n])). A [M,K] and B [N,K] are e4m3fn
  * bytes; scale_result and bias may be NULL.

@@ -11,6 +11,7 @@ import torch
 
 from _util import (assert_bits_equal, assert_close, bf16_to_f32, bits16, from_bits16, gen, u8)
 from oracle import act as oact
+from oracle import convrot as ocr
 from oracle import fp8 as of
 from oracle import int8 as oi
 from oracle import pair as op
@@ -168,6 +169,47 @@ def test_f16_outputs_round_f32_results_once(dev):
     ref = of.w8a16_linear(bits16(x), u8(wf), None, bits16(bw), "f16", x_dtype="f16",
                           out_dtype="f16")
     assert_bits_equal(bits16(y), ref, "w8a16 f16 out")
+
+
+# ConvRot: fused head merge + 256-wide rotation + rowwise quant
+MRQ_CASES = [(1, 24, 300, 128), (1, 12, 257, 256), (2, 3, 50, 256), (1, 8, 33, 96),
+             (1, 1, 5, 256), (1, 120, 3, 128)]
+
+
+def _bhsd(g, B, H, S, D):
+    x = torch.randn(B, H, S, D, generator=g) * torch.logspace(-3, 3, S)[None, None, :, None]
+    x[:, :, 0] = 0.0                          # an all-zero row: scale 1e-30, tiny bf16 divisor
+    return x.to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("rotate", [True, False])
+@pytest.mark.parametrize("B,H,S,D", MRQ_CASES)
+def test_merge_rot_quant_exact(dev, B, H, S, D, rotate):
+    g = gen(71 + B + H + S + D)
+    x = _bhsd(g, B, H, S, D)
+    q, sc = ops.i8_merge_rot_quant(x.to(dev), rotate)
+    assert q.shape == (B * S, H * D) and sc.shape == (B * S, 1)
+    rq, rs = ocr.merge_rot_quant(bits16(x), rotate)
+    assert_bits_equal(q.cpu().numpy(), rq, f"merge_rot_quant q {B}x{H}x{S}x{D} rot={rotate}")
+    assert_bits_equal(sc.cpu().numpy().reshape(-1).view(np.uint32),
+                      np.asarray(rs, np.float32).reshape(-1).view(np.uint32), "scales")
+
+
+def test_o_proj_prequant_chain_exact(dev):
+    """The reference's fused o-projection (int8_o_proj_prequant, per-channel
+    weight scales): merge + rotate + quant, then the fused_cs GEMM."""
+    g = gen(79)
+    B, H, S, D, N = 1, 24, 130, 128, 3072
+    x = _bhsd(g, B, H, S, D)
+    w = _randint8((N, H * D), g, -127, 128)
+    ws = torch.rand(N, generator=g) * 0.002
+    bias = torch.randn(N, generator=g).to(torch.bfloat16)
+    q, sc = ops.i8_merge_rot_quant(x.to(dev))
+    out = ops.i8_matmul2d_nt_fused_cs(q, w.to(dev), sc.reshape(-1), ws.to(dev), bias.to(dev))
+    rq, rs = ocr.merge_rot_quant(bits16(x))
+    ref = oi.epilogue_rowcolscale(oi.i8_matmul2d_nt(rq, w.numpy()), np.asarray(rs).reshape(-1),
+                                  ws.numpy(), bits16(bias))
+    assert_bits_equal(bits16(out), ref, "o_proj chain")
 
 
 # MOSS bf16 FC1/SiTU pair

@@ -21,6 +21,7 @@ import torch
 import torch.nn.functional as F
 
 from oracle import act as oact
+from oracle import convrot as ocr
 from oracle import fp8 as of
 from oracle import int8 as oi
 from oracle import pair as op
@@ -396,3 +397,59 @@ def test_cpu_baseline_paths_compute_the_oracle_results():
     ref = bf16_bits_to_f32(of.w8a16_linear(tbits(xb), wq.view(torch.uint8).numpy(),
                                            ws.reshape(1).numpy(), tbits(b)))
     assert (np.abs(cpu - ref) <= np.abs(ref) * 2.0 ** -7 + 1e-30).all()
+
+
+# ----------------------------------------------------------- ConvRot ---
+
+def _h256():
+    h = ocr.H4
+    return np.kron(h, np.kron(h, np.kron(h, h)))
+
+
+def test_h4_is_a_symmetric_hadamard_matrix():
+    h = _h256()
+    assert np.array_equal(ocr.H4, ocr.H4.T)
+    assert np.array_equal(h @ h.T, 256 * np.eye(256, dtype=np.int64))
+
+
+def test_fwht256_unit_vectors_give_the_kronecker_rows():
+    """One nonzero input: every sum is exact, so each output row must equal
+    the Kronecker power of H4 exactly (pins the stage strides, the digit
+    order and the H4 rows; the Sylvester H4 fails this)."""
+    got = ocr.fwht256(np.eye(256, dtype=np.float32))
+    assert np.array_equal(got.astype(np.int64), _h256())
+    sylv = np.array([[1, 1, 1, 1], [1, -1, 1, -1], [1, 1, -1, -1], [1, -1, -1, 1]])
+    assert not np.array_equal(np.kron(sylv, np.kron(sylv, np.kron(sylv, sylv))), _h256())
+
+
+def test_fwht256_random_is_the_matmul_within_fp32_rounding():
+    rng = np.random.default_rng(3)
+    v = rng.standard_normal((64, 256)).astype(np.float32)
+    exact = v.astype(np.float64) @ _h256().T.astype(np.float64)
+    got = ocr.fwht256(v)
+    assert np.abs(got - exact).max() <= 1e-5 * np.abs(exact).max()
+    # the butterfly order is observable: another association differs somewhere
+    w = v.copy()
+    idx = np.arange(256)
+    for stride in (1, 4, 16, 64):
+        digit = (idx // stride) % 4
+        base = idx - digit * stride
+        a = [w[:, base + k * stride] for k in range(4)]
+        sgn = ocr.H4[digit]
+        w = (a[0] * sgn[:, 0]).astype(np.float32) + ((a[1] * sgn[:, 1]) + ((a[2] * sgn[:, 2]) + (a[3] * sgn[:, 3])))
+    assert not np.array_equal(w.astype(np.float32), got)
+
+
+def test_merge_heads_is_the_torch_permute():
+    g = torch.Generator().manual_seed(40)
+    x = torch.randn(2, 3, 5, 128, generator=g).to(torch.bfloat16)
+    want = x.permute(0, 2, 1, 3).reshape(10, 384)
+    assert np.array_equal(ocr.merge_heads(tbits(x)), tbits(want))
+
+
+def test_merge_rot_quant_unrotated_is_rowwise_quant_of_the_merge():
+    g = torch.Generator().manual_seed(41)
+    x = torch.randn(1, 4, 7, 64, generator=g).to(torch.bfloat16)
+    q, s = ocr.merge_rot_quant(tbits(x), rotate=False)
+    q2, s2 = _torch_quant(x.permute(0, 2, 1, 3).reshape(7, 256))
+    assert np.array_equal(q, q2) and np.array_equal(s.reshape(-1), s2.reshape(-1))
