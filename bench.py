@@ -10,8 +10,9 @@ TFLOP/s (2*M*K*N per linear). ``roofline`` covers the dominant kernel of
 that step (the QKV W8A16 GEMM: one launch of whole rounds of 256x256 tiles
 plus one launch of the leftover tiles as split-K 64x64 pieces), timed with HIP
 events around each QKV call inside the timed region. ``per_config`` adds C1, C3, C4 and C5
-measured in the same process, plus MOSS_BF16 and WAN_FP16 (the bf16 FC1/SiTU
-pair and the fp16-output INT8 epilogue, not BASELINE configs); ``cpu_baseline`` times the reference's
+measured in the same process, plus MOSS_BF16, WAN_FP16 and CONVROT (the bf16
+FC1/SiTU pair, the fp16-output INT8 epilogue and the fused head-merge + ConvRot
++ quant pass; not BASELINE configs); ``cpu_baseline`` times the reference's
 PyTorch CPU path for C2 (kitchen dequant + bf16 F.linear) on a bounded row
 sample on this host's cores.
 
@@ -289,6 +290,23 @@ def bench_wan_fp16(torch, ops, dev, steps, warmup):
     return res
 
 
+def bench_convrot(torch, ops, dev, steps, warmup):
+    """Fused head merge + ConvRot + rowwise quant of an attention output
+    [1, H, S, D] (MiniMax H3 heads: D = 128, two heads per rotation group;
+    Ideogram: D = 256), HBM-bound: bytes = M*K*2 in + M*K out + M*4 scales."""
+    res = {}
+    for (H, S, D) in ((24, 9216, 128), (12, 9216, 256)):
+        g = torch.Generator(device=dev).manual_seed(8)
+        x = torch.randn(1, H, S, D, generator=g, device=dev).to(torch.bfloat16)
+        _, kern = Timer(torch).run(lambda p: marked(p, lambda: ops.i8_merge_rot_quant(x)),
+                                   max(5, steps // 2), max(2, warmup // 2))
+        byts = S * H * D * 3 + S * 4
+        res[f"H{H}_D{D}"] = {"shape": [1, H, S, D], "kernel_us": kern * 1e6,
+                             "gbs": byts / kern / 1e9, "frac_hbm": byts / kern / 1e9 / PEAK["hbm_gbs"]}
+        del x
+    return res
+
+
 # ----------------------------------------------------------------- C5 ---
 
 def bench_c5(torch, ops, dev, steps, warmup):
@@ -431,9 +449,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--only", default="C1,C2,C3,C4,C5,MOSS_BF16,WAN_FP16",
-                    help="comma list of configs to run (C2 is always run); MOSS_BF16 and "
-                         "WAN_FP16 time the widened rows (not BASELINE configs)")
+    ap.add_argument("--only", default="C1,C2,C3,C4,C5,MOSS_BF16,WAN_FP16,CONVROT",
+                    help="comma list of configs to run (C2 is always run); MOSS_BF16, "
+                         "WAN_FP16 and CONVROT time the widened rows (not BASELINE configs)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--pmc-target", action="store_true",
                     help="run the copy calibration and the C2 QKV kernel for rocprofv3 --pmc")
@@ -462,7 +480,8 @@ def main():
     c2 = bench_c2(torch, ops, dev, args.steps, args.warmup)
     torch.cuda.empty_cache()
     for name, fn in (("C1", bench_c1), ("C3", bench_c3), ("C4", bench_c4), ("C5", bench_c5),
-                     ("MOSS_BF16", bench_moss_bf16), ("WAN_FP16", bench_wan_fp16)):
+                     ("MOSS_BF16", bench_moss_bf16), ("WAN_FP16", bench_wan_fp16),
+                     ("CONVROT", bench_convrot)):
         if name in only:
             log(f"{name} ...")
             per[name] = fn(torch, ops, dev, args.steps, args.warmup)

@@ -32,6 +32,16 @@ __device__ __forceinline__ float block_max256(float v, float* red) {
 //   s     = T(scale), 0 -> finfo(T).tiny
 //   q     = int8(clamp(rint(T(x / s)), -128, 127))
 template <bool BF16>
+__device__ __forceinline__ uint32_t quant_i8(uint16_t h, float s) {
+  float v = round_half(half_f32(h, BF16) / s, BF16);
+  v = rintf(v);
+  v = fminf(fmaxf(v, -128.0f), 127.0f);
+  return (uint32_t)(uint8_t)(int8_t)(int)v;
+}
+
+// VEC: rows read 8 elements (16 bytes) and written 8 bytes at a time (the
+// entry point checks alignment, strides and K % 8).
+template <bool BF16, bool VEC>
 __global__ void __launch_bounds__(256)
 quant_rowwise_kernel(const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, float* scales,
                      int64_t K) {
@@ -39,63 +49,114 @@ quant_rowwise_kernel(const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, flo
   const int64_t row = blockIdx.x;
   const uint16_t* xr = x + row * ldx;
   float mx = 0.0f;
-  for (int64_t i = threadIdx.x; i < K; i += 256) mx = fmaxf(mx, fabsf(half_f32(xr[i], BF16)));
+  if constexpr (VEC) {
+    for (int64_t i = threadIdx.x * 8; i < K; i += 2048) {
+      const uint4 u = *reinterpret_cast<const uint4*>(xr + i);
+      const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        mx = fmaxf(mx, fmaxf(fabsf(half_f32((uint16_t)w[c], BF16)),
+                             fabsf(half_f32((uint16_t)(w[c] >> 16), BF16))));
+    }
+  } else {
+    for (int64_t i = threadIdx.x; i < K; i += 256) mx = fmaxf(mx, fabsf(half_f32(xr[i], BF16)));
+  }
   const float amax = block_max256(mx, red);
   const float scale = fmaxf(amax / 127.0f, 1e-30f);
   if (threadIdx.x == 0) scales[row] = scale;
   float s = round_half(scale, BF16);
   if (s == 0.0f) s = BF16 ? 1.1754943508222875e-38f : 6.103515625e-05f;
   int8_t* qr = q + row * ldq;
-  for (int64_t i = threadIdx.x; i < K; i += 256) {
-    float v = round_half(half_f32(xr[i], BF16) / s, BF16);
-    v = rintf(v);
-    v = fminf(fmaxf(v, -128.0f), 127.0f);
-    qr[i] = (int8_t)(int)v;
+  if constexpr (VEC) {
+    for (int64_t i = threadIdx.x * 8; i < K; i += 2048) {
+      const uint4 u = *reinterpret_cast<const uint4*>(xr + i);
+      const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+      uint32_t o[2];
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+        o[c] = quant_i8<BF16>((uint16_t)w[2 * c], s) |
+               (quant_i8<BF16>((uint16_t)(w[2 * c] >> 16), s) << 8) |
+               (quant_i8<BF16>((uint16_t)w[2 * c + 1], s) << 16) |
+               (quant_i8<BF16>((uint16_t)(w[2 * c + 1] >> 16), s) << 24);
+      *reinterpret_cast<uint2*>(qr + i) = uint2{o[0], o[1]};
+    }
+  } else {
+    for (int64_t i = threadIdx.x; i < K; i += 256) qr[i] = (int8_t)quant_i8<BF16>(xr[i], s);
   }
 }
 
 // Fused head merge + ConvRot + rowwise quant (reference
 // i8_merge_rot_quant_bf16, _patches/int8_ext/int8_gemm.mm:1429-1507): x
 // [B, H, S, D] bf16 contiguous; output row (b, s) of the merged [B*S, H*D]
-// matrix, element i = h*D + d. One workgroup per output row. With ROTATE,
-// every 256-element group is transformed by the radix-4 Walsh-Hadamard
-// butterflies at strides 1, 4, 16, 64 (row `digit` of
-// H4 = [[1,1,1,-1],[1,1,-1,1],[1,-1,1,1],[-1,1,1,1]] applied to the values at
-// base + k*stride, each sum in fp32 in the written order), scaled by 2^-4 and
-// rounded to bf16. Wave w takes groups w, w + 4, ...: lane l holds group
-// elements l + 64 j (j = 0..3), so the stride-64 stage is lane-local and the
-// other three stages go through a wave-private LDS row (no workgroup
-// barrier). The rotated row stays in LDS for the quant pass, which is the
-// rowwise arithmetic above.
+// matrix, element i = h*D + d. One workgroup per output row, in three
+// passes over the row held in LDS:
+//   1. gather: the H head runs of D elements, 16 bytes per load (all loads
+//      of the row in flight at once) where D and x allow, else 2 bytes;
+//   2. with ROTATE, every 256-element group is transformed in place by the
+//      radix-4 Walsh-Hadamard butterflies at strides 1, 4, 16, 64 (row
+//      `digit` of H4 = [[1,1,1,-1],[1,1,-1,1],[1,-1,1,1],[-1,1,1,1]] applied
+//      to the values at base + k*stride, each sum in fp32 in the written
+//      order), scaled by 2^-4 and rounded to bf16. Wave w takes groups w,
+//      w + 4, ...: lane l holds group elements l + 64 j (j = 0..3), so the
+//      stride-64 stage is lane-local and the other three go through a
+//      wave-private LDS row (no workgroup barrier);
+//   3. the rowwise quant arithmetic above, 16 outputs per thread stored as
+//      one 16-byte write where q allows.
+// Row `digit` of H4 negates operand 3 - digit. Each row is the reference's
+// expression (a0 + a1 + a2 - a3, a0 + a1 - a2 + a3, a0 - a1 + a2 + a3,
+// -a0 + a1 + a2 + a3, summed left to right): x - y is x + (-y) exactly, so
+// flipping one sign bit and adding in the same order gives the same bits,
+// without a branch on the lane's digit.
 __device__ __forceinline__ float h4_row(int digit, float a0, float a1, float a2, float a3) {
-  if (digit == 0) return a0 + a1 + a2 - a3;
-  if (digit == 1) return a0 + a1 - a2 + a3;
-  if (digit == 2) return a0 - a1 + a2 + a3;
-  return -a0 + a1 + a2 + a3;
+  const uint32_t sgn = 0x80000000u;
+  a0 = bits_f32(f32_bits(a0) ^ (digit == 3 ? sgn : 0u));
+  a1 = bits_f32(f32_bits(a1) ^ (digit == 2 ? sgn : 0u));
+  a2 = bits_f32(f32_bits(a2) ^ (digit == 1 ? sgn : 0u));
+  a3 = bits_f32(f32_bits(a3) ^ (digit == 0 ? sgn : 0u));
+  return ((a0 + a1) + a2) + a3;
+}
+
+__device__ __forceinline__ uint32_t quant_byte(uint16_t r, float sc) {
+  float v = round_half(bf16_f32(r) / sc, true);
+  v = rintf(v);
+  v = fminf(fmaxf(v, -128.0f), 127.0f);
+  return (uint32_t)(uint8_t)(int8_t)(int)v;
 }
 
 template <bool ROTATE>
 __global__ void __launch_bounds__(256)
 merge_rot_quant_kernel(const uint16_t* x, int64_t H, int64_t S, int64_t D, int8_t* q,
-                       float* scales) {
-  extern __shared__ uint16_t rot[];            // the row's H*D rotated bf16 values
+                       float* scales, int vec_x, int vec_q) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t rot[];   // the row, H*D bf16
   __shared__ float work[4][256];
   __shared__ float red[4];
   const int64_t row = blockIdx.x;
   const int64_t b = row / S, s = row - b * S;
-  const int64_t K = H * D;
-  const int groups = (int)(K >> 8);
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int K = (int)(H * D);
+  const int groups = K >> 8;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const uint16_t* xr = x + (b * H * S + s) * D;        // head h at xr + h * S * D
+  const int64_t hstride = S * D;
+  const int d_ = (int)D;
+  if (vec_x) {
+    for (int i = tid * 8; i < K; i += 2048) {
+      const int h = i / d_, d = i - h * d_;
+      *reinterpret_cast<uint4*>(rot + i) = *reinterpret_cast<const uint4*>(xr + h * hstride + d);
+    }
+  } else {
+    for (int i = tid; i < K; i += 256) {
+      const int h = i / d_, d = i - h * d_;
+      rot[i] = xr[h * hstride + d];
+    }
+  }
+  __syncthreads();
   float* w = work[wave];
   float mx = 0.0f;
   for (int g = wave; g < groups; g += 4) {
+    uint16_t* grp = rot + g * 256;
     float v[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t i = (int64_t)g * 256 + lane + 64 * j;
-      const int64_t h = i / D, d = i - h * D;
-      v[j] = bf16_f32(x[((b * H + h) * S + s) * D + d]);
-    }
+    for (int j = 0; j < 4; ++j) v[j] = bf16_f32(grp[lane + 64 * j]);
     if constexpr (ROTATE) {
 #pragma unroll
       for (int stride = 1; stride <= 16; stride *= 4) {
@@ -111,29 +172,40 @@ merge_rot_quant_kernel(const uint16_t* x, int64_t H, int64_t S, int64_t D, int8_
         }
         lds_fence_wave();
       }
-      // stride 64: the four values of the group are this lane's v[0..3],
-      // and element l + 64 j has digit j
+      // stride 64: the group's four values are this lane's v[0..3], and
+      // element l + 64 j has digit j
       const float a0 = v[0], a1 = v[1], a2 = v[2], a3 = v[3];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) v[j] = bf16_f32(bf16_rte(h4_row(j, a0, a1, a2, a3) * 0.0625f));
+      for (int j = 0; j < 4; ++j) {
+        const uint16_t r = bf16_rte(h4_row(j, a0, a1, a2, a3) * 0.0625f);
+        grp[lane + 64 * j] = r;
+        v[j] = bf16_f32(r);
+      }
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      rot[g * 256 + lane + 64 * j] = (uint16_t)(f32_bits(v[j]) >> 16);   // v[j] is a bf16 value
-      mx = fmaxf(mx, fabsf(v[j]));
-    }
+    for (int j = 0; j < 4; ++j) mx = fmaxf(mx, fabsf(v[j]));
   }
-  const float amax = block_max256(mx, red);    // also orders the rot writes before the reads
+  const float amax = block_max256(mx, red);    // its barrier also publishes the rotated row
   const float scale = fmaxf(amax / 127.0f, 1e-30f);
-  if (threadIdx.x == 0) scales[row] = scale;
+  if (tid == 0) scales[row] = scale;
   float sc = round_half(scale, true);
   if (sc == 0.0f) sc = 1.1754943508222875e-38f;
-  int8_t* qr = q + row * K;
-  for (int64_t i = threadIdx.x; i < K; i += 256) {
-    float r = round_half(bf16_f32(rot[i]) / sc, true);
-    r = rintf(r);
-    r = fminf(fmaxf(r, -128.0f), 127.0f);
-    qr[i] = (int8_t)(int)r;
+  int8_t* qr = q + row * (int64_t)K;
+  if (vec_q) {
+    for (int i = tid * 16; i < K; i += 4096) {
+      const uint4 lo = *reinterpret_cast<const uint4*>(rot + i);
+      const uint4 hi = *reinterpret_cast<const uint4*>(rot + i + 8);
+      const uint32_t h16[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+      uint32_t out[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        out[c] = quant_byte((uint16_t)h16[2 * c], sc) | (quant_byte((uint16_t)(h16[2 * c] >> 16), sc) << 8) |
+                 (quant_byte((uint16_t)h16[2 * c + 1], sc) << 16) |
+                 (quant_byte((uint16_t)(h16[2 * c + 1] >> 16), sc) << 24);
+      *reinterpret_cast<uint4*>(qr + i) = uint4{out[0], out[1], out[2], out[3]};
+    }
+  } else {
+    for (int i = tid; i < K; i += 256) qr[i] = (int8_t)quant_byte(rot[i], sc);
   }
 }
 
@@ -141,22 +213,43 @@ __global__ void fill_zero_kernel(float* p) { p[0] = 0.0f; }
 
 // amax of |x| over n elements into *amax (bits of a non-negative float
 // compare like unsigned integers, so atomicMax on the bits is a float max).
-template <bool BF16>
+// VEC: x 16-byte aligned; the first n & ~7 elements are read 8 at a time.
+template <bool BF16, bool VEC>
 __global__ void __launch_bounds__(256)
 absmax_kernel(const uint16_t* x, int64_t n, float* amax) {
   __shared__ float red[4];
   float mx = 0.0f;
   const int64_t stride = (int64_t)gridDim.x * 256;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride)
-    mx = fmaxf(mx, fabsf(half_f32(x[i], BF16)));
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  int64_t done = 0;
+  if constexpr (VEC) {
+    const int64_t n8 = n >> 3;
+    for (int64_t i = t; i < n8; i += stride) {
+      const uint4 u = *reinterpret_cast<const uint4*>(x + i * 8);
+      const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        mx = fmaxf(mx, fmaxf(fabsf(half_f32((uint16_t)w[c], BF16)),
+                             fabsf(half_f32((uint16_t)(w[c] >> 16), BF16))));
+    }
+    done = n8 * 8;
+  }
+  for (int64_t i = done + t; i < n; i += stride) mx = fmaxf(mx, fabsf(half_f32(x[i], BF16)));
   mx = block_max256(mx, red);
   if (threadIdx.x == 0) atomicMax(reinterpret_cast<unsigned int*>(amax), __float_as_uint(mx));
 }
 
 // q = e4m3fn(clamp(x / scale, -448, 448)); scale = amax / 448, or 1 for an
 // all-zero tensor. NaN passes the clamp and encodes as NaN, as torch's
-// clamp-then-cast does.
+// clamp-then-cast does. VEC: x 16-byte and q 8-byte aligned.
 template <bool BF16>
+__device__ __forceinline__ uint32_t quant_e4m3(uint16_t h, float s) {
+  float v = half_f32(h, BF16) / s;
+  v = v > 448.0f ? 448.0f : (v < -448.0f ? -448.0f : v);
+  return f32_e4m3(v);
+}
+
+template <bool BF16, bool VEC>
 __global__ void __launch_bounds__(256)
 quant_pertensor_kernel(const uint16_t* x, int64_t n, uint8_t* q, float* scale,
                        const float* amax) {
@@ -164,11 +257,25 @@ quant_pertensor_kernel(const uint16_t* x, int64_t n, uint8_t* q, float* scale,
   if (s == 0.0f) s = 1.0f;
   if (blockIdx.x == 0 && threadIdx.x == 0) scale[0] = s;
   const int64_t stride = (int64_t)gridDim.x * 256;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) {
-    float v = half_f32(x[i], BF16) / s;
-    v = v > 448.0f ? 448.0f : (v < -448.0f ? -448.0f : v);
-    q[i] = f32_e4m3(v);
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  int64_t done = 0;
+  if constexpr (VEC) {
+    const int64_t n8 = n >> 3;
+    for (int64_t i = t; i < n8; i += stride) {
+      const uint4 u = *reinterpret_cast<const uint4*>(x + i * 8);
+      const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+      uint32_t o[2];
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+        o[c] = quant_e4m3<BF16>((uint16_t)w[2 * c], s) |
+               (quant_e4m3<BF16>((uint16_t)(w[2 * c] >> 16), s) << 8) |
+               (quant_e4m3<BF16>((uint16_t)w[2 * c + 1], s) << 16) |
+               (quant_e4m3<BF16>((uint16_t)(w[2 * c + 1] >> 16), s) << 24);
+      *reinterpret_cast<uint2*>(q + i * 8) = uint2{o[0], o[1]};
+    }
+    done = n8 * 8;
   }
+  for (int64_t i = done + t; i < n; i += stride) q[i] = (uint8_t)quant_e4m3<BF16>(x[i], s);
 }
 
 // fp8 -> T dequant with the same conversion routine the W8A16 GEMM uses
@@ -224,12 +331,15 @@ extern "C" int c4q_i8_quant_rowwise(const void* x, int x_dtype, int64_t ldx, int
   C4Q_REQUIRE(M < (1ll << 31), C4Q_ERR_SHAPE, "%s: too many rows", what);
   hipStream_t s = as_stream(stream);
   const uint16_t* xs = static_cast<const uint16_t*>(x);
+  const bool vec = aligned16(xs) && ldx % 8 == 0 && K % 8 == 0 &&
+                   (reinterpret_cast<uintptr_t>(q) & 7u) == 0 && ldq % 8 == 0;
+  auto launch = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, dim3((unsigned)M), dim3(256), 0, s, xs, ldx, q, ldq, scales, K);
+  };
   if (x_dtype == C4Q_BF16)
-    hipLaunchKernelGGL(quant_rowwise_kernel<true>, dim3((unsigned)M), dim3(256), 0, s, xs, ldx, q,
-                       ldq, scales, K);
+    vec ? launch(quant_rowwise_kernel<true, true>) : launch(quant_rowwise_kernel<true, false>);
   else
-    hipLaunchKernelGGL(quant_rowwise_kernel<false>, dim3((unsigned)M), dim3(256), 0, s, xs, ldx, q,
-                       ldq, scales, K);
+    vec ? launch(quant_rowwise_kernel<false, true>) : launch(quant_rowwise_kernel<false, false>);
   return check_launch(what);
 }
 
@@ -251,12 +361,14 @@ extern "C" int c4q_i8_merge_rot_quant(const uint16_t* x, int64_t B, int64_t H, i
   C4Q_REQUIRE(x && q && scales, C4Q_ERR_ARG, "%s: null pointer", what);
   hipStream_t s = as_stream(stream);
   const size_t lds = (size_t)K * 2;
+  const int vec_x = aligned16(x) && D % 8 == 0;      // every head run: whole 16-byte chunks
+  const int vec_q = aligned16(q);                     // rows of K bytes, K a multiple of 256
   if (rotate)
     hipLaunchKernelGGL(merge_rot_quant_kernel<true>, dim3((unsigned)M), dim3(256), lds, s, x, H, S,
-                       D, q, scales);
+                       D, q, scales, vec_x, vec_q);
   else
     hipLaunchKernelGGL(merge_rot_quant_kernel<false>, dim3((unsigned)M), dim3(256), lds, s, x, H, S,
-                       D, q, scales);
+                       D, q, scales, vec_x, vec_q);
   return check_launch(what);
 }
 
@@ -269,16 +381,19 @@ extern "C" int c4q_f8_quant_pertensor(const void* x, int x_dtype, int64_t n, uin
   C4Q_REQUIRE(scale && amax_ws && (n == 0 || (x && q)), C4Q_ERR_ARG, "%s: null pointer", what);
   hipStream_t s = as_stream(stream);
   const uint16_t* xs = static_cast<const uint16_t*>(x);
-  const int g = grid_for(n);
+  const bool vec = aligned16(xs) && (reinterpret_cast<uintptr_t>(q) & 7u) == 0;
+  const int g = grid_for(vec ? cdiv(n, 8) : n);
   hipLaunchKernelGGL(fill_zero_kernel, dim3(1), dim3(1), 0, s, amax_ws);
+  auto run = [&](auto amax_k, auto quant_k) {
+    hipLaunchKernelGGL(amax_k, dim3(g), dim3(256), 0, s, xs, n, amax_ws);
+    hipLaunchKernelGGL(quant_k, dim3(g), dim3(256), 0, s, xs, n, q, scale, amax_ws);
+  };
   if (x_dtype == C4Q_BF16) {
-    hipLaunchKernelGGL(absmax_kernel<true>, dim3(g), dim3(256), 0, s, xs, n, amax_ws);
-    hipLaunchKernelGGL(quant_pertensor_kernel<true>, dim3(g), dim3(256), 0, s, xs, n, q, scale,
-                       amax_ws);
+    if (vec) run(absmax_kernel<true, true>, quant_pertensor_kernel<true, true>);
+    else run(absmax_kernel<true, false>, quant_pertensor_kernel<true, false>);
   } else {
-    hipLaunchKernelGGL(absmax_kernel<false>, dim3(g), dim3(256), 0, s, xs, n, amax_ws);
-    hipLaunchKernelGGL(quant_pertensor_kernel<false>, dim3(g), dim3(256), 0, s, xs, n, q, scale,
-                       amax_ws);
+    if (vec) run(absmax_kernel<false, true>, quant_pertensor_kernel<false, true>);
+    else run(absmax_kernel<false, false>, quant_pertensor_kernel<false, false>);
   }
   return check_launch(what);
 }

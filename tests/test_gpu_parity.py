@@ -173,7 +173,7 @@ def test_f16_outputs_round_f32_results_once(dev):
 
 # ConvRot: fused head merge + 256-wide rotation + rowwise quant
 MRQ_CASES = [(1, 24, 300, 128), (1, 12, 257, 256), (2, 3, 50, 256), (1, 8, 33, 96),
-             (1, 1, 5, 256), (1, 120, 3, 128)]
+             (1, 1, 5, 256), (1, 120, 3, 128), (1, 64, 9, 100)]   # D=100: 2-byte gathers
 
 
 def _bhsd(g, B, H, S, D):
@@ -191,6 +191,21 @@ def test_merge_rot_quant_exact(dev, B, H, S, D, rotate):
     assert q.shape == (B * S, H * D) and sc.shape == (B * S, 1)
     rq, rs = ocr.merge_rot_quant(bits16(x), rotate)
     assert_bits_equal(q.cpu().numpy(), rq, f"merge_rot_quant q {B}x{H}x{S}x{D} rot={rotate}")
+    assert_bits_equal(sc.cpu().numpy().reshape(-1).view(np.uint32),
+                      np.asarray(rs, np.float32).reshape(-1).view(np.uint32), "scales")
+
+
+def test_merge_rot_quant_unaligned_input(dev):
+    """x at a 2-byte offset takes the 2-byte gathers."""
+    g = gen(77)
+    B, H, S, D = 1, 6, 40, 128
+    x = _bhsd(g, B, H, S, D)
+    flat = torch.empty(x.numel() + 1, dtype=torch.bfloat16, device=dev)
+    xd = flat[1:].view(B, H, S, D)
+    xd.copy_(x.to(dev))
+    q, sc = ops.i8_merge_rot_quant(xd)
+    rq, rs = ocr.merge_rot_quant(bits16(x))
+    assert_bits_equal(q.cpu().numpy(), rq, "merge_rot_quant unaligned q")
     assert_bits_equal(sc.cpu().numpy().reshape(-1).view(np.uint32),
                       np.asarray(rs, np.float32).reshape(-1).view(np.uint32), "scales")
 
@@ -308,6 +323,30 @@ def test_quant_rowwise_exact(dev, dtype, M, K):
     qr, sr = oi.quant_rowwise(bits16(x), "bf16" if dtype == torch.bfloat16 else "f16")
     assert_bits_equal(q.cpu().numpy(), qr, "q")
     assert_bits_equal(s.cpu().numpy().reshape(-1).view(np.uint32), sr.view(np.uint32), "scale")
+
+
+def test_quant_rowwise_strided_and_offset(dev):
+    """Row stride not a multiple of 8, and rows at a 2-byte offset: the
+    2-byte path."""
+    g = gen(9)
+    x = (torch.randn(40, 1027, generator=g) * 3).to(torch.bfloat16)
+    xs = x.to(dev)[:, :1024]
+    q, s = ops.i8_quant_rowwise(xs)
+    qr, sr = oi.quant_rowwise(bits16(x[:, :1024]), "bf16")
+    assert_bits_equal(q.cpu().numpy(), qr, "strided q")
+    flat = torch.empty(40 * 1024 + 1, dtype=torch.bfloat16, device=dev)
+    xo = flat[1:].view(40, 1024)
+    xo.copy_(x[:, :1024].to(dev))
+    q, s = ops.i8_quant_rowwise(xo)
+    assert_bits_equal(q.cpu().numpy(), qr, "offset q")
+    assert_bits_equal(s.cpu().numpy().reshape(-1).view(np.uint32), sr.view(np.uint32), "scale")
+    flat8 = torch.empty(40 * 1024 + 3, dtype=torch.bfloat16, device=dev)
+    xf = flat8[3:].view(-1)
+    xf.copy_(x[:, :1024].reshape(-1).to(dev))
+    qf, sf = ops.fp8_quant_pertensor(xf)
+    qfr, sfr = of.quant_pertensor(bits16(x[:, :1024].reshape(-1)))
+    assert sf.item() == sfr
+    assert_bits_equal(u8(qf), qfr, "fp8 quant offset")
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
