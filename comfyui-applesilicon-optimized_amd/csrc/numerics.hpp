@@ -62,6 +62,22 @@ C4Q_HD float f16_f32(uint16_t h) {
   return bits_f32(sign | ((e + 112u) << 23) | (m << 13));
 }
 
+// bf16(RN(x / s)) without a division per element, for bf16 values x and a
+// positive normal bf16 s, given r = RN(1 / s). Both significands have 8
+// bits, so x/s either lies exactly on a bf16 rounding midpoint or at least
+// 2^-9 / 255 (relative) away from every midpoint; q0 = RN(x r) is within
+// about 2^-23 of x/s, and the residual step q1 = RN(q0 - RN(q0 s - x) r)
+// (both fused, the residual exact) lands exactly on such a midpoint. So
+// bf16 rounding of q1 equals bf16 rounding of the correctly rounded
+// quotient; checked for every pair of bf16 x and s with |x/s| < 2^64 on the
+// GPU (tests/test_gpu_numerics.py). The residual is formed as q0 s - x and
+// subtracted so that x = -0 gives -0 (x - q0 s would give +0).
+C4Q_HD float div_bf16_operands(float x, float s, float r) {
+  const float q0 = x * r;
+  const float e = __builtin_fmaf(q0, s, -x);
+  return __builtin_fmaf(-e, r, q0);
+}
+
 // fp8 e4m3fn code -> float (exact). 0x7F / 0xFF are NaN; no infinities.
 C4Q_HD float e4m3_f32(uint32_t c) {
   uint32_t sign = (c & 0x80u) << 24;

@@ -31,9 +31,13 @@ __device__ __forceinline__ float block_max256(float v, float* red) {
 //   scale = max(amax / 127, 1e-30)  (fp32, correctly rounded divide; stored)
 //   s     = T(scale), 0 -> finfo(T).tiny
 //   q     = int8(clamp(rint(T(x / s)), -128, 127))
+// T(x / s) with the row's divisor s (a T value) and its reciprocal r: bf16
+// rows use the reciprocal quotient (div_bf16_operands, equal after bf16
+// rounding to the correctly rounded quotient); f16 rows divide.
 template <bool BF16>
-__device__ __forceinline__ uint32_t quant_i8(uint16_t h, float s) {
-  float v = round_half(half_f32(h, BF16) / s, BF16);
+__device__ __forceinline__ uint32_t quant_i8(uint16_t h, float s, float r) {
+  const float x = half_f32(h, BF16);
+  float v = round_half(BF16 ? div_bf16_operands(x, s, r) : x / s, BF16);
   v = rintf(v);
   v = fminf(fmaxf(v, -128.0f), 127.0f);
   return (uint32_t)(uint8_t)(int8_t)(int)v;
@@ -66,6 +70,7 @@ quant_rowwise_kernel(const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, flo
   if (threadIdx.x == 0) scales[row] = scale;
   float s = round_half(scale, BF16);
   if (s == 0.0f) s = BF16 ? 1.1754943508222875e-38f : 6.103515625e-05f;
+  const float rs = 1.0f / s;
   int8_t* qr = q + row * ldq;
   if constexpr (VEC) {
     for (int64_t i = threadIdx.x * 8; i < K; i += 2048) {
@@ -74,14 +79,14 @@ quant_rowwise_kernel(const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, flo
       uint32_t o[2];
 #pragma unroll
       for (int c = 0; c < 2; ++c)
-        o[c] = quant_i8<BF16>((uint16_t)w[2 * c], s) |
-               (quant_i8<BF16>((uint16_t)(w[2 * c] >> 16), s) << 8) |
-               (quant_i8<BF16>((uint16_t)w[2 * c + 1], s) << 16) |
-               (quant_i8<BF16>((uint16_t)(w[2 * c + 1] >> 16), s) << 24);
+        o[c] = quant_i8<BF16>((uint16_t)w[2 * c], s, rs) |
+               (quant_i8<BF16>((uint16_t)(w[2 * c] >> 16), s, rs) << 8) |
+               (quant_i8<BF16>((uint16_t)w[2 * c + 1], s, rs) << 16) |
+               (quant_i8<BF16>((uint16_t)(w[2 * c + 1] >> 16), s, rs) << 24);
       *reinterpret_cast<uint2*>(qr + i) = uint2{o[0], o[1]};
     }
   } else {
-    for (int64_t i = threadIdx.x; i < K; i += 256) qr[i] = (int8_t)quant_i8<BF16>(xr[i], s);
+    for (int64_t i = threadIdx.x; i < K; i += 256) qr[i] = (int8_t)quant_i8<BF16>(xr[i], s, rs);
   }
 }
 
@@ -116,19 +121,32 @@ __device__ __forceinline__ float h4_row(int digit, float a0, float a1, float a2,
   return ((a0 + a1) + a2) + a3;
 }
 
-__device__ __forceinline__ uint32_t quant_byte(uint16_t r, float sc) {
-  float v = round_half(bf16_f32(r) / sc, true);
-  v = rintf(v);
-  v = fminf(fmaxf(v, -128.0f), 127.0f);
-  return (uint32_t)(uint8_t)(int8_t)(int)v;
+
+// Two radix-4 stages of the Walsh-Hadamard transform on 16 values held by
+// one lane: v[4 hi + lo] with `lo` the digit of the first stage and `hi` the
+// digit of the second (each output the reference's row expression).
+__device__ __forceinline__ void h4_two_stages(float (&v)[16]) {
+  float t[16];
+#pragma unroll
+  for (int hi = 0; hi < 4; ++hi)
+#pragma unroll
+    for (int lo = 0; lo < 4; ++lo)
+      t[4 * hi + lo] = h4_row(lo, v[4 * hi], v[4 * hi + 1], v[4 * hi + 2], v[4 * hi + 3]);
+#pragma unroll
+  for (int lo = 0; lo < 4; ++lo)
+#pragma unroll
+    for (int hi = 0; hi < 4; ++hi)
+      v[4 * hi + lo] = h4_row(hi, t[lo], t[4 + lo], t[8 + lo], t[12 + lo]);
 }
+
+constexpr int kRotSlot = 256 + 16;   // floats per group slot of a wave (padding spreads banks)
 
 template <bool ROTATE>
 __global__ void __launch_bounds__(256)
 merge_rot_quant_kernel(const uint16_t* x, int64_t H, int64_t S, int64_t D, int8_t* q,
                        float* scales, int vec_x, int vec_q) {
   extern __shared__ __attribute__((aligned(16))) uint16_t rot[];   // the row, H*D bf16
-  __shared__ float work[4][256];
+  __shared__ __attribute__((aligned(16))) float work[4][4 * kRotSlot];
   __shared__ float red[4];
   const int64_t row = blockIdx.x;
   const int64_t b = row / S, s = row - b * S;
@@ -150,46 +168,62 @@ merge_rot_quant_kernel(const uint16_t* x, int64_t H, int64_t S, int64_t D, int8_
     }
   }
   __syncthreads();
-  float* w = work[wave];
+  // A wave takes 4 groups at a time, 16 lanes each: lane c = lane & 15 of
+  // slot gq = lane >> 4 first holds elements 16 c + m (m = 0..15; the
+  // stride-1 and stride-4 digits are the two digits of m), then, after a
+  // transpose through the wave's LDS slots, elements c + 16 m (the stride-16
+  // and stride-64 digits).
   float mx = 0.0f;
-  for (int g = wave; g < groups; g += 4) {
+  const int gq = lane >> 4, c = lane & 15;
+  float* slot = work[wave] + gq * kRotSlot;
+  for (int g0 = wave * 4; g0 < groups; g0 += 16) {
+    const int g = g0 + gq;
+    const bool live = g < groups;
     uint16_t* grp = rot + g * 256;
-    float v[4];
+    float v[16];
+    if (live) {
+      const uint4 lo = *reinterpret_cast<const uint4*>(grp + 16 * c);
+      const uint4 hi = *reinterpret_cast<const uint4*>(grp + 16 * c + 8);
+      const uint32_t w[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) v[j] = bf16_f32(grp[lane + 64 * j]);
-    if constexpr (ROTATE) {
-#pragma unroll
-      for (int stride = 1; stride <= 16; stride *= 4) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) w[lane + 64 * j] = v[j];
-        lds_fence_wave();
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int idx = lane + 64 * j;
-          const int digit = (idx / stride) & 3;
-          const int base = idx - digit * stride;
-          v[j] = h4_row(digit, w[base], w[base + stride], w[base + 2 * stride], w[base + 3 * stride]);
-        }
-        lds_fence_wave();
-      }
-      // stride 64: the group's four values are this lane's v[0..3], and
-      // element l + 64 j has digit j
-      const float a0 = v[0], a1 = v[1], a2 = v[2], a3 = v[3];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint16_t r = bf16_rte(h4_row(j, a0, a1, a2, a3) * 0.0625f);
-        grp[lane + 64 * j] = r;
-        v[j] = bf16_f32(r);
+      for (int k = 0; k < 8; ++k) {
+        v[2 * k] = bf16_f32((uint16_t)w[k]);
+        v[2 * k + 1] = bf16_f32((uint16_t)(w[k] >> 16));
       }
     }
+    if constexpr (ROTATE) {
+      if (live) {
+        h4_two_stages(v);                                   // strides 1 and 4
 #pragma unroll
-    for (int j = 0; j < 4; ++j) mx = fmaxf(mx, fabsf(v[j]));
+        for (int k = 0; k < 4; ++k)
+          *reinterpret_cast<float4*>(slot + 16 * c + 4 * k) =
+              make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
+      }
+      lds_fence_wave();
+      if (live) {
+#pragma unroll
+        for (int m = 0; m < 16; ++m) v[m] = slot[c + 16 * m];
+        h4_two_stages(v);                                   // strides 16 and 64
+#pragma unroll
+        for (int m = 0; m < 16; ++m) {
+          const uint16_t r = bf16_rte(v[m] * 0.0625f);
+          grp[c + 16 * m] = r;
+          v[m] = bf16_f32(r);
+        }
+      }
+      lds_fence_wave();                                     // slots free for the next groups
+    }
+    if (live) {
+#pragma unroll
+      for (int m = 0; m < 16; ++m) mx = fmaxf(mx, fabsf(v[m]));
+    }
   }
   const float amax = block_max256(mx, red);    // its barrier also publishes the rotated row
   const float scale = fmaxf(amax / 127.0f, 1e-30f);
   if (tid == 0) scales[row] = scale;
   float sc = round_half(scale, true);
   if (sc == 0.0f) sc = 1.1754943508222875e-38f;
+  const float rc = 1.0f / sc;
   int8_t* qr = q + row * (int64_t)K;
   if (vec_q) {
     for (int i = tid * 16; i < K; i += 4096) {
@@ -199,13 +233,14 @@ merge_rot_quant_kernel(const uint16_t* x, int64_t H, int64_t S, int64_t D, int8_
       uint32_t out[4];
 #pragma unroll
       for (int c = 0; c < 4; ++c)
-        out[c] = quant_byte((uint16_t)h16[2 * c], sc) | (quant_byte((uint16_t)(h16[2 * c] >> 16), sc) << 8) |
-                 (quant_byte((uint16_t)h16[2 * c + 1], sc) << 16) |
-                 (quant_byte((uint16_t)(h16[2 * c + 1] >> 16), sc) << 24);
+        out[c] = quant_i8<true>((uint16_t)h16[2 * c], sc, rc) |
+                 (quant_i8<true>((uint16_t)(h16[2 * c] >> 16), sc, rc) << 8) |
+                 (quant_i8<true>((uint16_t)h16[2 * c + 1], sc, rc) << 16) |
+                 (quant_i8<true>((uint16_t)(h16[2 * c + 1] >> 16), sc, rc) << 24);
       *reinterpret_cast<uint4*>(qr + i) = uint4{out[0], out[1], out[2], out[3]};
     }
   } else {
-    for (int i = tid; i < K; i += 256) qr[i] = (int8_t)quant_byte(rot[i], sc);
+    for (int i = tid; i < K; i += 256) qr[i] = (int8_t)quant_i8<true>(rot[i], sc, rc);
   }
 }
 

@@ -55,6 +55,38 @@ extern "C" int c4q_probe_cvt_exhaustive(int which, unsigned long long* out, void
   return (int)hipGetLastError();
 }
 
+// Every non-NaN bf16 x and every positive normal bf16 s with |x/s| < 2^64:
+// bf16 rounding of div_bf16_operands(x, s, RN(1/s)) against bf16 rounding of
+// the IEEE quotient. Thread t: x = t >> 8, s = 0x0080 + 128 (t & 255) + k.
+__global__ void __launch_bounds__(256) div_bf16_all(unsigned long long* bad, uint32_t* first) {
+  const uint32_t t = blockIdx.x * 256u + threadIdx.x;
+  const uint32_t xb = t >> 8;
+  if ((xb & 0x7FFFu) > 0x7F80u) return;                     // NaN x
+  const float x = bf16_f32((uint16_t)xb);
+  unsigned long long n = 0;
+  for (uint32_t k = 0; k < 128; ++k) {
+    const uint32_t sb = 0x0080u + 128u * (t & 255u) + k;
+    if (sb > 0x7F7Fu) break;                                 // positive normal bf16 only
+    const float s = bf16_f32((uint16_t)sb);
+    const float exact = x / s;
+    if (!(fabsf(exact) < 1.8446744073709552e19f)) continue;  // |x/s| >= 2^64
+    const float r = 1.0f / s;
+    if (bf16_rte(div_bf16_operands(x, s, r)) != bf16_rte(exact)) {
+      if (n == 0) atomicMin(first, (xb << 16) | sb);
+      ++n;
+    }
+  }
+  if (n) atomicAdd(bad, n);
+}
+
+// out: device [2] u64 (mismatch count, first mismatching pair x << 16 | s).
+extern "C" int c4q_probe_div_bf16_exhaustive(unsigned long long* out, void* stream) {
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  uint32_t* first = reinterpret_cast<uint32_t*>(out + 1);
+  hipLaunchKernelGGL(div_bf16_all, dim3(65536), dim3(256), 0, s, out, first);
+  return (int)hipGetLastError();
+}
+
 // ---------------------------------------------------------- tile plans ---
 // Host-side enumeration of the launches a GEMM's tile plan issues
 // (plan_launches, tile_at -- the functions the library runs). cover
