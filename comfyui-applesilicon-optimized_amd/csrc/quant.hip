@@ -11,8 +11,10 @@ namespace {
 __device__ __forceinline__ float half_f32(uint16_t h, bool bf16) {
   return bf16 ? bf16_f32(h) : f16_f32(h);
 }
+// T rounding (RNE) of v as a float; bf16 through v_cvt_pk_bf16_f32, which
+// equals bf16_rte for every non-NaN float (checked on all 2^32 inputs).
 __device__ __forceinline__ float round_half(float v, bool bf16) {
-  return bf16 ? bf16_f32(bf16_rte(v)) : f16_f32(f16_rte(v));
+  return bf16 ? bf16lo(bf16x2_rne(v, 0.0f)) : f16_f32(f16_rte(v));
 }
 
 // Max over the 256 threads of a workgroup (values are >= 0).
@@ -45,7 +47,9 @@ __device__ __forceinline__ uint32_t quant_i8(uint16_t h, float s, float r) {
 
 // VEC: rows read 8 elements (16 bytes) and written 8 bytes at a time (the
 // entry point checks alignment, strides and K % 8).
-template <bool BF16, bool VEC>
+// CACHE (with VEC, K <= 8192): each thread keeps its at most four 8-element
+// chunks of the row in registers, so the row is read once.
+template <bool BF16, bool VEC, bool CACHE>
 __global__ void __launch_bounds__(256)
 quant_rowwise_kernel(const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, float* scales,
                      int64_t K) {
@@ -53,6 +57,43 @@ quant_rowwise_kernel(const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, flo
   const int64_t row = blockIdx.x;
   const uint16_t* xr = x + row * ldx;
   float mx = 0.0f;
+  if constexpr (CACHE) {
+    uint4 u[4];
+    const int k0 = (int)threadIdx.x * 8;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      if (k0 + 2048 * c < K) u[c] = *reinterpret_cast<const uint4*>(xr + k0 + 2048 * c);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      if (k0 + 2048 * c >= K) continue;
+      const uint32_t w[4] = {u[c].x, u[c].y, u[c].z, u[c].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        mx = fmaxf(mx, fmaxf(fabsf(half_f32((uint16_t)w[e], BF16)),
+                             fabsf(half_f32((uint16_t)(w[e] >> 16), BF16))));
+    }
+    const float amax = block_max256(mx, red);
+    const float scale = fmaxf(amax / 127.0f, 1e-30f);
+    if (threadIdx.x == 0) scales[row] = scale;
+    float s = round_half(scale, BF16);
+    if (s == 0.0f) s = BF16 ? 1.1754943508222875e-38f : 6.103515625e-05f;
+    const float rs = 1.0f / s;
+    int8_t* qr = q + row * ldq;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      if (k0 + 2048 * c >= K) continue;
+      const uint32_t w[4] = {u[c].x, u[c].y, u[c].z, u[c].w};
+      uint32_t o[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        o[h] = quant_i8<BF16>((uint16_t)w[2 * h], s, rs) |
+               (quant_i8<BF16>((uint16_t)(w[2 * h] >> 16), s, rs) << 8) |
+               (quant_i8<BF16>((uint16_t)w[2 * h + 1], s, rs) << 16) |
+               (quant_i8<BF16>((uint16_t)(w[2 * h + 1] >> 16), s, rs) << 24);
+      *reinterpret_cast<uint2*>(qr + k0 + 2048 * c) = uint2{o[0], o[1]};
+    }
+    return;
+  }
   if constexpr (VEC) {
     for (int64_t i = threadIdx.x * 8; i < K; i += 2048) {
       const uint4 u = *reinterpret_cast<const uint4*>(xr + i);
@@ -205,10 +246,12 @@ merge_rot_quant_kernel(const uint16_t* x, int64_t H, int64_t S, int64_t D, int8_
         for (int m = 0; m < 16; ++m) v[m] = slot[c + 16 * m];
         h4_two_stages(v);                                   // strides 16 and 64
 #pragma unroll
-        for (int m = 0; m < 16; ++m) {
-          const uint16_t r = bf16_rte(v[m] * 0.0625f);
-          grp[c + 16 * m] = r;
-          v[m] = bf16_f32(r);
+        for (int m = 0; m < 16; m += 2) {
+          const uint32_t p = bf16x2_rne(v[m] * 0.0625f, v[m + 1] * 0.0625f);
+          grp[c + 16 * m] = (uint16_t)p;
+          grp[c + 16 * (m + 1)] = (uint16_t)(p >> 16);
+          v[m] = bf16lo(p);
+          v[m + 1] = bf16hi(p);
         }
       }
       lds_fence_wave();                                     // slots free for the next groups
@@ -368,13 +411,19 @@ extern "C" int c4q_i8_quant_rowwise(const void* x, int x_dtype, int64_t ldx, int
   const uint16_t* xs = static_cast<const uint16_t*>(x);
   const bool vec = aligned16(xs) && ldx % 8 == 0 && K % 8 == 0 &&
                    (reinterpret_cast<uintptr_t>(q) & 7u) == 0 && ldq % 8 == 0;
+  const bool cache = vec && K <= 8192;
   auto launch = [&](auto kernel) {
     hipLaunchKernelGGL(kernel, dim3((unsigned)M), dim3(256), 0, s, xs, ldx, q, ldq, scales, K);
   };
-  if (x_dtype == C4Q_BF16)
-    vec ? launch(quant_rowwise_kernel<true, true>) : launch(quant_rowwise_kernel<true, false>);
-  else
-    vec ? launch(quant_rowwise_kernel<false, true>) : launch(quant_rowwise_kernel<false, false>);
+  if (x_dtype == C4Q_BF16) {
+    if (cache) launch(quant_rowwise_kernel<true, true, true>);
+    else if (vec) launch(quant_rowwise_kernel<true, true, false>);
+    else launch(quant_rowwise_kernel<true, false, false>);
+  } else {
+    if (cache) launch(quant_rowwise_kernel<false, true, true>);
+    else if (vec) launch(quant_rowwise_kernel<false, true, false>);
+    else launch(quant_rowwise_kernel<false, false, false>);
+  }
   return check_launch(what);
 }
 
