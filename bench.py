@@ -11,8 +11,8 @@ that step (the QKV W8A16 GEMM: one launch of whole rounds of 256x256 tiles
 plus one launch of the leftover tiles as split-K 64x64 pieces), timed with HIP
 events around each QKV call inside the timed region. ``per_config`` adds C1, C3, C4 and C5
 measured in the same process, plus MOSS_BF16, WAN_FP16 and CONVROT (the bf16
-FC1/SiTU pair, the fp16-output INT8 epilogue and the fused head-merge + ConvRot
-+ quant pass; not BASELINE configs); ``cpu_baseline`` times the reference's
+FC1/SiTU pair, the fp16-output INT8 epilogue, the fused head-merge + ConvRot
++ quant pass and the SwiGLU + ConvRot pass; not BASELINE configs); ``cpu_baseline`` times the reference's
 PyTorch CPU path for C2 (kitchen dequant + bf16 F.linear) on a bounded row
 sample on this host's cores.
 
@@ -304,6 +304,16 @@ def bench_convrot(torch, ops, dev, steps, warmup):
         res[f"H{H}_D{D}"] = {"shape": [1, H, S, D], "kernel_us": kern * 1e6,
                              "gbs": byts / kern / 1e9, "frac_hbm": byts / kern / 1e9 / PEAK["hbm_gbs"]}
         del x
+    # SwiGLU + rotation of an fc1 output [M, 2F] (the INT8 fc2 pre-pass)
+    M, F = 9216, 8192
+    x = torch.randn(M, 2 * F, generator=torch.Generator(device=dev).manual_seed(9),
+                    device=dev).to(torch.bfloat16)
+    ops.i8_swiglu_rot(x)
+    _, kern = Timer(torch).run(lambda p: marked(p, lambda: ops.i8_swiglu_rot(x)),
+                               max(5, steps // 2), max(2, warmup // 2))
+    byts = M * 2 * F * 2 + M * F * 2
+    res[f"swiglu_rot_M{M}_F{F}"] = {"kernel_us": kern * 1e6, "gbs": byts / kern / 1e9,
+                                     "frac_hbm": byts / kern / 1e9 / PEAK["hbm_gbs"]}
     return res
 
 

@@ -182,6 +182,35 @@ __device__ __forceinline__ void h4_two_stages(float (&v)[16]) {
 
 constexpr int kRotSlot = 256 + 16;   // floats per group slot of a wave (padding spreads banks)
 
+// The rotation of one 256-element group by a team of 16 lanes (c = lane &
+// 15): on entry lane c holds elements 16 c + m in v[m] (the stride-1 and
+// stride-4 digits are the two digits of m); on return it holds the
+// transformed elements c + 16 m (times 2^-4, rounded to bf16), having passed
+// through `slot` (the team's 256 + 16 floats of LDS) once. Every lane of the
+// wave calls it (`live` false: the lane only keeps the wave in step).
+__device__ __forceinline__ void rot_group16(float (&v)[16], float* slot, int c, bool live) {
+  if (live) {
+    h4_two_stages(v);                                       // strides 1 and 4
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      *reinterpret_cast<float4*>(slot + 16 * c + 4 * k) =
+          make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
+  }
+  lds_fence_wave();
+  if (live) {
+#pragma unroll
+    for (int m = 0; m < 16; ++m) v[m] = slot[c + 16 * m];
+    h4_two_stages(v);                                       // strides 16 and 64
+#pragma unroll
+    for (int m = 0; m < 16; m += 2) {
+      const uint32_t p = bf16x2_rne(v[m] * 0.0625f, v[m + 1] * 0.0625f);
+      v[m] = bf16lo(p);
+      v[m + 1] = bf16hi(p);
+    }
+  }
+  lds_fence_wave();                                         // slot free again
+}
+
 template <bool ROTATE>
 __global__ void __launch_bounds__(256)
 merge_rot_quant_kernel(const uint16_t* x, int64_t H, int64_t S, int64_t D, int8_t* q,
@@ -233,28 +262,11 @@ merge_rot_quant_kernel(const uint16_t* x, int64_t H, int64_t S, int64_t D, int8_
       }
     }
     if constexpr (ROTATE) {
-      if (live) {
-        h4_two_stages(v);                                   // strides 1 and 4
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-          *reinterpret_cast<float4*>(slot + 16 * c + 4 * k) =
-              make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
-      }
-      lds_fence_wave();
+      rot_group16(v, slot, c, live);
       if (live) {
 #pragma unroll
-        for (int m = 0; m < 16; ++m) v[m] = slot[c + 16 * m];
-        h4_two_stages(v);                                   // strides 16 and 64
-#pragma unroll
-        for (int m = 0; m < 16; m += 2) {
-          const uint32_t p = bf16x2_rne(v[m] * 0.0625f, v[m + 1] * 0.0625f);
-          grp[c + 16 * m] = (uint16_t)p;
-          grp[c + 16 * (m + 1)] = (uint16_t)(p >> 16);
-          v[m] = bf16lo(p);
-          v[m + 1] = bf16hi(p);
-        }
+        for (int m = 0; m < 16; ++m) grp[c + 16 * m] = (uint16_t)(f32_bits(v[m]) >> 16);
       }
-      lds_fence_wave();                                     // slots free for the next groups
     }
     if (live) {
 #pragma unroll
@@ -284,6 +296,62 @@ merge_rot_quant_kernel(const uint16_t* x, int64_t H, int64_t S, int64_t D, int8_
     }
   } else {
     for (int i = tid; i < K; i += 256) qr[i] = (int8_t)quant_i8<true>(rot[i], sc, rc);
+  }
+}
+
+// SwiGLU + ConvRot pre-pass of an H3 INT8 fc2 (reference i8_swiglu_rot_bf16,
+// _patches/int8_ext/int8_gemm.mm:1521-1554): x [M, 2F] bf16 rows (gate
+// columns [0, F), up columns [F, 2F)) -> rot [M, F] bf16 with
+//   act = bf16(f32(SiLU[a]) * f32(b))   (SiLU: the 65,536-entry bf16 table)
+// rotated per 256-element group as in merge_rot_quant_kernel. One workgroup
+// per row; a wave takes 4 groups at a time, 16 lanes each; the rotated group
+// goes back through the team's LDS slot so that each lane stores 16
+// consecutive outputs (two 16-byte writes).
+__global__ void __launch_bounds__(256)
+swiglu_rot_kernel(const uint16_t* x, int64_t F, const uint16_t* silu, uint16_t* rot) {
+  __shared__ __attribute__((aligned(16))) float work[4][4 * kRotSlot];
+  const int64_t row = blockIdx.x;
+  const uint16_t* xr = x + row * 2 * F;
+  uint16_t* rr = rot + row * F;
+  const int groups = (int)(F >> 8);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int gq = lane >> 4, c = lane & 15;
+  float* slot = work[wave] + gq * kRotSlot;
+  for (int g0 = wave * 4; g0 < groups; g0 += 16) {
+    const int g = g0 + gq;
+    const bool live = g < groups;
+    float v[16];
+    if (live) {
+      const uint16_t* ga = xr + g * 256 + 16 * c;
+      const uint4 a0 = *reinterpret_cast<const uint4*>(ga);
+      const uint4 a1 = *reinterpret_cast<const uint4*>(ga + 8);
+      const uint4 b0 = *reinterpret_cast<const uint4*>(ga + F);
+      const uint4 b1 = *reinterpret_cast<const uint4*>(ga + F + 8);
+      const uint32_t wa[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+      const uint32_t wb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const float s0 = bf16_f32(silu[wa[k] & 0xFFFFu]), s1 = bf16_f32(silu[wa[k] >> 16]);
+        const uint32_t p = bf16x2_rne(s0 * bf16lo(wb[k]), s1 * bf16hi(wb[k]));
+        v[2 * k] = bf16lo(p);
+        v[2 * k + 1] = bf16hi(p);
+      }
+    }
+    rot_group16(v, slot, c, live);
+    // back through the slot (bf16 bits) to 16 consecutive outputs per lane
+    uint16_t* bslot = reinterpret_cast<uint16_t*>(slot);
+    if (live) {
+#pragma unroll
+      for (int m = 0; m < 16; ++m) bslot[c + 16 * m] = (uint16_t)(f32_bits(v[m]) >> 16);
+    }
+    lds_fence_wave();
+    if (live) {
+      const uint4 o0 = *reinterpret_cast<const uint4*>(bslot + 16 * c);
+      const uint4 o1 = *reinterpret_cast<const uint4*>(bslot + 16 * c + 8);
+      *reinterpret_cast<uint4*>(rr + g * 256 + 16 * c) = o0;
+      *reinterpret_cast<uint4*>(rr + g * 256 + 16 * c + 8) = o1;
+    }
+    lds_fence_wave();
   }
 }
 
@@ -453,6 +521,22 @@ extern "C" int c4q_i8_merge_rot_quant(const uint16_t* x, int64_t B, int64_t H, i
   else
     hipLaunchKernelGGL(merge_rot_quant_kernel<false>, dim3((unsigned)M), dim3(256), lds, s, x, H, S,
                        D, q, scales, vec_x, vec_q);
+  return check_launch(what);
+}
+
+extern "C" int c4q_i8_swiglu_rot(const uint16_t* x, int64_t M, int64_t F,
+                                 const uint16_t* silu_table, uint16_t* rot, void* stream) {
+  const char* what = "c4q_i8_swiglu_rot";
+  C4Q_REQUIRE(M >= 0 && F >= 0 && F % 256 == 0, C4Q_ERR_SHAPE,
+              "%s: need M >= 0 and F a multiple of 256 (M=%lld F=%lld)", what, (long long)M,
+              (long long)F);
+  if (M == 0 || F == 0) return C4Q_OK;
+  C4Q_REQUIRE(M < (1ll << 31), C4Q_ERR_SHAPE, "%s: too many rows", what);
+  C4Q_REQUIRE(x && rot && silu_table, C4Q_ERR_ARG, "%s: null pointer", what);
+  C4Q_REQUIRE(aligned16(x) && aligned16(rot), C4Q_ERR_ARG, "%s: x and rot must be 16-byte aligned",
+              what);
+  hipLaunchKernelGGL(swiglu_rot_kernel, dim3((unsigned)M), dim3(256), 0, as_stream(stream), x, F,
+                     silu_table, rot);
   return check_launch(what);
 }
 

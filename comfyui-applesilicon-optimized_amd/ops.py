@@ -6,7 +6,8 @@ RuntimeError before any work is enqueued):
 
     i8_matmul2d_nt, i8_matmul2d_nt_fused, i8_matmul2d_nt_fused_cs,
     i8_matmul2d_nt_fused_cs_half,
-    i8_quant_rowwise, i8_merge_rot_quant (_patches/int8_ext/int8_gemm.mm:2626-2715)
+    i8_quant_rowwise, i8_merge_rot_quant, i8_swiglu_rot
+                                     (_patches/int8_ext/int8_gemm.mm:2626-2715)
     fp8fp8_matmul2d_nt               (_patches/fp8_ext/fp8_matmul2d.mm:229-265)
     w8a16_f32, w8a16_bias_bf16       (_patches/fp8s_ext/w8a16_gemm.mm:286-329)
 
@@ -201,6 +202,27 @@ def i8_merge_rot_quant(x, rotate=True):
         _lib.call("c4q_i8_merge_rot_quant", x.data_ptr(), B, H, S, D, 1 if rotate else 0,
                   q.data_ptr(), scales.data_ptr(), _stream(dev))
     return q, scales
+
+
+def i8_swiglu_rot(x, silu_table=None):
+    """x [M, 2F] bf16 contiguous -> [M, F] bf16: SwiGLU (bf16 SiLU of the gate
+    half times the up half, in bf16) rotated per 256-element ConvRot group
+    (_patches/int8_ext/int8_gemm.mm:2593-2631). silu_table defaults to the
+    device's bf16 SiLU table (ops.act_table("silu"))."""
+    _req(x.dtype == torch.bfloat16, "x must be bf16")
+    _req(x.dim() == 2 and x.is_contiguous(), "x must be contiguous [M,2F]")
+    M, W = x.shape
+    _req(W % 512 == 0, "F must be a multiple of convrot groupsize 256")
+    dev = _dev(x, silu_table)
+    t = silu_table if silu_table is not None else act_table("silu", dev)
+    _req(t.numel() == 65536 and t.element_size() == 2 and t.is_contiguous(),
+         "silu_table must be 65536 contiguous 16-bit entries")
+    F = W // 2
+    rot = torch.empty((M, F), dtype=torch.bfloat16, device=dev)
+    with _on(dev):
+        _lib.call("c4q_i8_swiglu_rot", x.data_ptr(), M, F, t.data_ptr(), rot.data_ptr(),
+                  _stream(dev))
+    return rot
 
 
 def i8_quant_rowwise(x):

@@ -106,6 +106,16 @@ int c4q_i8_quant_rowwise(const void* x, int x_dtype, int64_t ldx, int8_t* q, int
 int c4q_i8_merge_rot_quant(const uint16_t* x, int64_t B, int64_t H, int64_t S, int64_t D,
                            int rotate, int8_t* q, float* scales, void* stream);
 
+/* SwiGLU + ConvRot pre-pass of an INT8 fc2: x [M, 2F] bf16 contiguous
+ * (gate columns [0,F), up columns [F,2F)), F a multiple of 256 ->
+ * rot [M, F] bf16 contiguous, act = bf16(f32(silu_table[a]) * f32(b))
+ * rotated per 256-element group as in c4q_i8_merge_rot_quant. silu_table:
+ * 65,536 bf16 entries (SiLU of every bf16 value). x and rot 16-byte aligned.
+ * Replaces i8_swiglu_rot (_patches/int8_ext/int8_gemm.mm:2593-2631, kernel
+ * :1521-1554), called by the INT8 fc2 path (_patches/int8_linear_kernel_mps.py:756-770). */
+int c4q_i8_swiglu_rot(const uint16_t* x, int64_t M, int64_t F, const uint16_t* silu_table,
+                      uint16_t* rot, void* stream);
+
 /* torch._scaled_mm fp8 route: D[M,N] = out_dtype(((f32(A@B^T) * scale_a)
  * * scale_b) * scale_result + f32(bias[n])). A [M,K] and B [N,K] are e4m3fn
  * bytes; scale_result and bias may be NULL.

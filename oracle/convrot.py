@@ -23,6 +23,7 @@ in the reference tree, so that equivalence is parity unpinned here.
 """
 import numpy as np
 
+from .act import apply_table
 from .int8 import quant_rowwise
 from .numerics import F32, bf16_bits_to_f32, f32_to_bf16_bits
 
@@ -71,3 +72,19 @@ def merge_rot_quant(x_bits, rotate=True):
     if rotate:
         xm = rotate_bf16(xm)
     return quant_rowwise(xm, "bf16")
+
+
+def swiglu_rot(x_bits, silu_table):
+    """The reference's ``i8_swiglu_rot(x)`` (``int8_gemm.mm:1521-1554``, host
+    ``:2593-2631``): x [M, 2F] bf16, act = bf16(f32(bf16 SiLU(a)) * f32(b))
+    with a the gate columns [0, F) and b the up columns [F, 2F) (the bf16 op
+    sequence of silu_mul_split_bf16), then every 256-element group of act
+    rotated as in ``rotate_bf16``. The SiLU is the bf16 table given (torch's
+    F.silu over every bf16 value in the tests; the reference evaluates
+    a / (1 + exp(-a)) with Metal's precise::exp, whose last-ulp agreement
+    with that table is parity unpinned)."""
+    x = np.asarray(x_bits)
+    f = x.shape[1] // 2
+    a = bf16_bits_to_f32(apply_table(silu_table, x[:, :f]))
+    act = f32_to_bf16_bits(a * bf16_bits_to_f32(x[:, f:]))
+    return rotate_bf16(act)

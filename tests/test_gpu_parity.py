@@ -227,6 +227,34 @@ def test_o_proj_prequant_chain_exact(dev):
     assert_bits_equal(bits16(out), ref, "o_proj chain")
 
 
+@pytest.mark.parametrize("M,F", [(130, 8192), (1, 256), (37, 768), (9, 4352)])
+def test_swiglu_rot_exact(dev, M, F):
+    g = gen(81 + M + F)
+    x = (torch.randn(M, 2 * F, generator=g) * torch.logspace(-2, 2, M)[:, None]).to(torch.bfloat16)
+    silu = torch.from_numpy(oact.silu_table().view(np.int16))
+    rot = ops.i8_swiglu_rot(x.to(dev), silu.to(dev))
+    assert rot.shape == (M, F) and rot.dtype == torch.bfloat16
+    assert_bits_equal(bits16(rot), ocr.swiglu_rot(bits16(x), oact.silu_table()),
+                      f"swiglu_rot {M}x{F}")
+
+
+def test_fc2_swiglu_rot_chain_exact(dev):
+    """The reference's INT8 fc2 route (int8_linear_kernel_mps.py:756-770):
+    swiglu_rot, rowwise quant, fused INT8 GEMM with per-channel scales."""
+    g = gen(83)
+    M, F, N = 96, 1024, 512
+    x = (torch.randn(M, 2 * F, generator=g) * 2).to(torch.bfloat16)
+    w = _randint8((N, F), g, -127, 128)
+    ws = torch.rand(N, generator=g) * 0.002
+    silu = torch.from_numpy(oact.silu_table().view(np.int16)).to(dev)
+    rot = ops.i8_swiglu_rot(x.to(dev), silu)
+    q, sc = ops.i8_quant_rowwise(rot)
+    out = ops.i8_matmul2d_nt_fused_cs(q, w.to(dev), sc.reshape(-1), ws.to(dev))
+    rq, rs = oi.quant_rowwise(ocr.swiglu_rot(bits16(x), oact.silu_table()), "bf16")
+    ref = oi.epilogue_rowcolscale(oi.i8_matmul2d_nt(rq, w.numpy()), rs.reshape(-1), ws.numpy())
+    assert_bits_equal(bits16(out), ref, "fc2 chain")
+
+
 # MOSS bf16 FC1/SiTU pair
 def _moss_tables(dev):
     return tuple(torch.from_numpy(t.view(np.int16)).to(dev) for t in oact.situ_tables())

@@ -453,3 +453,14 @@ def test_merge_rot_quant_unrotated_is_rowwise_quant_of_the_merge():
     q, s = ocr.merge_rot_quant(tbits(x), rotate=False)
     q2, s2 = _torch_quant(x.permute(0, 2, 1, 3).reshape(7, 256))
     assert np.array_equal(q, q2) and np.array_equal(s.reshape(-1), s2.reshape(-1))
+
+
+def test_swiglu_rot_is_torch_swiglu_then_the_rotation():
+    g = torch.Generator().manual_seed(42)
+    x = (torch.randn(6, 1024, generator=g) * 3).to(torch.bfloat16)
+    act = F.silu(x[:, :512]) * x[:, 512:]                      # bf16 ops, torch CPU
+    got = ocr.swiglu_rot(tbits(x), oact.silu_table())
+    assert np.array_equal(got, ocr.rotate_bf16(tbits(act)))
+    # gate and up swapped (a plausible mistake) differs
+    xs = torch.cat([x[:, 512:], x[:, :512]], dim=1)
+    assert not np.array_equal(ocr.swiglu_rot(tbits(xs), oact.silu_table()), got)
