@@ -25,9 +25,18 @@ Mirrors ``_patches/int8_linear_kernel_mps.py`` (and the int8-fast seam of
   reference re-routes them to a bf16 dequant + F.linear on MPS; on MI355X
   the int8 kernel is the fast path).
 
-Not supported here (those calls keep the original function): ConvRot
-activation rotation (``convrot=True``; comfy_kitchen's Hadamard rounding is
-not pinned), non-int8 weights, tensors off the ROCm device.
+* ``int8_o_proj_prequant`` is the fused o-projection from the attention
+  layout (``:436-535``): head merge + ConvRot + rowwise quant in one kernel
+  (``ops.i8_merge_rot_quant``), then the fused INT8 GEMM;
+* ``_try_int8_swiglu_forward`` is ``linear(swiglu(x))`` (``:708-775``): for a
+  ConvRot weight the fused SwiGLU + rotation pass (``ops.i8_swiglu_rot``),
+  rowwise quant and the INT8 GEMM; otherwise the bf16 SwiGLU and the
+  ordinary W8A8 path.
+
+Not supported here (those calls keep the original function): the generic
+ConvRot rotation of ``int8_linear(..., convrot=True)`` (comfy_kitchen's eager
+Hadamard matmul; its rounding is not pinned), non-int8 weights, tensors off
+the ROCm device.
 """
 import os
 import weakref
@@ -137,6 +146,79 @@ def _try_int8_kernel_forward(self, input):
     if input.dtype not in (torch.bfloat16, torch.float16):
         return None
     return _int8_linear_kernel(input, w._qdata, params.scale, self.bias, input.dtype)
+
+
+def _plain_int8_layer(layer):
+    """The weight/flag part of the reference's eligibility gates."""
+    w = getattr(layer, "weight", None)
+    if not _common.is_quantized_int8(w):
+        return None
+    if getattr(layer, "_full_precision_mm", False) or getattr(layer, "comfy_force_cast_weights", False):
+        return None
+    if len(getattr(layer, "weight_function", [])) or len(getattr(layer, "bias_function", [])):
+        return None
+    if getattr(w._params, "transposed", False):
+        return None
+    return w
+
+
+def int8_o_proj_prequant(layer, out_bhsd):
+    """o-projection straight from the attention layout [B, H, S, D]
+    (reference ``:436-535``): bf16 [B, S, N], or None when a check fails
+    (the caller then merges heads and runs the layer). The rotation is
+    always the fused butterfly pass -- the reference's mode "2"; its mode "1"
+    for D = 256 rotates with comfy_kitchen's eager Hadamard matmul, which this
+    build does not have (same rounding class, different fp32 sum order).
+    ``C4Q_INT8_OPROJ_FUSE=0`` (or the reference's ``ASFP8_INT8_OPROJ_FUSE=0``)
+    turns it off."""
+    mode = os.environ.get("C4Q_INT8_OPROJ_FUSE", os.environ.get("ASFP8_INT8_OPROJ_FUSE", "1"))
+    if mode == "0":
+        return None
+    if (not isinstance(out_bhsd, torch.Tensor) or out_bhsd.dim() != 4
+            or not _common.on_device(out_bhsd) or out_bhsd.dtype != torch.bfloat16):
+        return None
+    w = _plain_int8_layer(layer)
+    if w is None:
+        return None
+    params = w._params
+    if not getattr(params, "convrot", False) or getattr(params, "convrot_groupsize", 256) != 256:
+        return None
+    B, H, S, D = out_bhsd.shape
+    qdata = w._qdata
+    if D <= 0 or D > 256 or (H * D) % 256 or H * D * 2 > 30 * 1024 or H * D != qdata.shape[1]:
+        return None
+    x_8, x_scale = ops.i8_merge_rot_quant(out_bhsd.contiguous())
+    return _int8_linear_prequant(x_8, x_scale, qdata.contiguous(), params.scale, layer.bias,
+                                 torch.bfloat16, (B, S, H * D))
+
+
+def _try_int8_swiglu_forward(linear, x):
+    """``linear(swiglu(x))`` (reference ``:708-775``), or None to fall back.
+    With a ConvRot weight (group size 256) and a contiguous bf16 input: the
+    fused SwiGLU + rotation pass, rowwise quant, the INT8 GEMM; without
+    ConvRot: the bf16 SwiGLU (torch ops) and the ordinary kernel path."""
+    if not _common.on_device(x) or _common.is_quantized_int8(x):
+        return None
+    w = _plain_int8_layer(linear)
+    if w is None:
+        return None
+    wide = x.shape[-1]
+    if wide % 2 or x.dtype not in (torch.bfloat16, torch.float16):
+        return None
+    half = wide // 2
+    params = w._params
+    if getattr(params, "convrot", False):
+        x2 = x.reshape(-1, wide)
+        if (getattr(params, "convrot_groupsize", 256) != 256 or x.dtype != torch.bfloat16
+                or not x2.is_contiguous() or half % 256
+                or os.environ.get("C4Q_INT8_SWIGLU_ROT", "1") == "0"):
+            return None
+        rot = ops.i8_swiglu_rot(x2)
+        x_8, x_scale = ops.i8_quant_rowwise(rot)
+        return _int8_linear_prequant(x_8, x_scale, w._qdata, params.scale, linear.bias, x.dtype,
+                                     (*x.shape[:-1], half), split_tail=True)
+    act = torch.nn.functional.silu(x[..., :half]) * x[..., half:]
+    return _int8_linear_kernel(act, w._qdata, params.scale, linear.bias, x.dtype)
 
 
 # ---------------------------------------------------------- int8-fast seam ---

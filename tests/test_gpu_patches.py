@@ -166,3 +166,42 @@ def test_moss_bf16_project_exact(dev):
     rows = slice(0, 4096, 37)                   # the oracle on a row sample (seconds, not minutes)
     ref = op.moss_bf16_pair(bits16(x[0, rows]), bits16(w), *oact.situ_tables())
     assert_bits_equal(bits16(out[0, rows]), ref, "moss bf16 project")
+
+
+def test_o_proj_prequant_and_swiglu_forward_exact(dev):
+    """The two ConvRot routes of the INT8 linear patch on a stand-in
+    TensorWiseINT8Layout weight, bit-exact against the oracle chains."""
+    import types
+    from oracle import convrot as ocr
+
+    class QT:
+        _layout_cls = "TensorWiseINT8Layout"
+
+        def __init__(self, q, scale):
+            self._qdata = q
+            self._params = types.SimpleNamespace(scale=scale, convrot=True, transposed=False,
+                                                 convrot_groupsize=256)
+
+    g = gen(31)
+    B, H, S, D, N = 1, 8, 70, 128, 384
+    x = (torch.randn(B, H, S, D, generator=g) * 3).to(torch.bfloat16)
+    w = _i8((N, H * D), g)
+    ws = torch.rand(N, generator=g) * 0.002
+    layer = types.SimpleNamespace(weight=QT(w.to(dev), ws.to(dev)), bias=None, weight_function=[],
+                                  bias_function=[])
+    out = int8_linear.int8_o_proj_prequant(layer, x.to(dev))
+    assert out.shape == (B, S, N)
+    rq, rs = ocr.merge_rot_quant(bits16(x))
+    ref = oi.epilogue_rowcolscale(oi.i8_matmul2d_nt(rq, w.numpy()), rs.reshape(-1), ws.numpy())
+    assert_bits_equal(bits16(out.reshape(S, N)), ref, "o_proj patch")
+    F = 512
+    xf = (torch.randn(2, 35, 2 * F, generator=g) * 2).to(torch.bfloat16)
+    w2 = _i8((N, F), g)
+    lin = types.SimpleNamespace(weight=QT(w2.to(dev), ws.to(dev)), bias=None, weight_function=[],
+                                bias_function=[])
+    y = int8_linear._try_int8_swiglu_forward(lin, xf.to(dev))
+    assert y.shape == (2, 35, N)
+    silu_dev = ops.act_table("silu", dev).cpu().numpy().view(np.uint16)
+    rq2, rs2 = oi.quant_rowwise(ocr.swiglu_rot(bits16(xf.reshape(70, 2 * F)), silu_dev), "bf16")
+    ref2 = oi.epilogue_rowcolscale(oi.i8_matmul2d_nt(rq2, w2.numpy()), rs2.reshape(-1), ws.numpy())
+    assert_bits_equal(bits16(y.reshape(70, N)), ref2, "swiglu fc2 patch")

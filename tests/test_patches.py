@@ -189,6 +189,43 @@ def test_try_int8_kernel_forward_eligibility(cpu_gate, monkeypatch):
     assert len(fake.calls) == 1
 
 
+def test_o_proj_prequant_gate(cpu_gate, monkeypatch):
+    calls = {}
+    monkeypatch.setattr(ops, "i8_merge_rot_quant",
+                        lambda x: calls.setdefault("mrq", (torch.zeros(x.shape[0] * x.shape[2], x.shape[1] * x.shape[3], dtype=torch.int8),
+                                                           torch.ones(x.shape[0] * x.shape[2], 1))))
+    monkeypatch.setattr(int8_linear, "_int8_linear_prequant",
+                        lambda x_8, x_scale, w, ws, b, dt, shape, split_tail=False: ("gemm", shape))
+    x = torch.zeros(1, 4, 5, 128, dtype=torch.bfloat16)
+    q = _i8((16, 512), 1)
+    f = int8_linear.int8_o_proj_prequant
+    assert f(_layer(FakeQT(q, torch.rand(16), convrot=True)), x) == ("gemm", (1, 5, 512))
+    assert f(_layer(FakeQT(q, torch.rand(16))), x) is None                 # not ConvRot
+    assert f(_layer(FakeQT(q, torch.rand(16), convrot=True)), x.float()) is None
+    assert f(_layer(FakeQT(_i8((16, 384), 1), torch.rand(16), convrot=True)),
+             torch.zeros(1, 3, 5, 128, dtype=torch.bfloat16)) is None     # 384 % 256
+    assert f(_layer(FakeQT(q, torch.rand(16), convrot=True, transposed=True)), x) is None
+    monkeypatch.setenv("C4Q_INT8_OPROJ_FUSE", "0")
+    assert f(_layer(FakeQT(q, torch.rand(16), convrot=True)), x) is None
+
+
+def test_swiglu_forward_routes(cpu_gate, monkeypatch):
+    seen = []
+    monkeypatch.setattr(ops, "i8_swiglu_rot", lambda x2: seen.append("rot") or torch.zeros(x2.shape[0], x2.shape[1] // 2, dtype=torch.bfloat16))
+    monkeypatch.setattr(ops, "i8_quant_rowwise", lambda r: (torch.zeros(r.shape, dtype=torch.int8), torch.ones(r.shape[0], 1)))
+    monkeypatch.setattr(int8_linear, "_int8_linear_prequant",
+                        lambda x_8, x_scale, w, ws, b, dt, shape, split_tail=False: ("prequant", shape))
+    monkeypatch.setattr(int8_linear, "_int8_linear_kernel", lambda act, *a: ("kernel", tuple(act.shape)))
+    x = torch.randn(2, 3, 1024).to(torch.bfloat16)
+    q = _i8((8, 512), 1)
+    f = int8_linear._try_int8_swiglu_forward
+    assert f(_layer(FakeQT(q, torch.rand(8), convrot=True)), x) == ("prequant", (2, 3, 512))
+    assert seen == ["rot"]
+    assert f(_layer(FakeQT(q, torch.rand(8))), x) == ("kernel", (2, 3, 512))
+    assert f(_layer(FakeQT(q, torch.rand(8), convrot=True)), x[..., :1000]) is None   # 500 % 256
+    assert f(_layer(q), x) is None
+
+
 def test_int8_fast_seam_uses_w8a8(cpu_gate, monkeypatch):
     rec = _fake_int8_ops(monkeypatch)
     x = torch.randn(40, 16).to(torch.bfloat16)
