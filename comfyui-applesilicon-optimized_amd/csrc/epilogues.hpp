@@ -20,6 +20,9 @@
 //   value4(m, n, v, nv)        = apply(rowp(m), col(n, nv), v)
 //   row(m), vec                byte pointer to output row m; rows are
 //                              16-byte aligned (chunked stores allowed)
+//   addr(m, n)                 byte address of output (m, n): row(m) + n
+//                              elements, or a functor's own layout (columns
+//                              n .. n+7 from a multiple of 8 are contiguous)
 //   kColFields, col_raw(f, n, N), col_val(f, w), row_raw(m, M)
 //                              the same parameters as raw words, one column
 //                              or row per call: col_raw / row_raw only load
@@ -110,6 +113,9 @@ struct EpiOut {
   void* d; int64_t ldd; int vec;
   __device__ __forceinline__ uint8_t* row(int64_t m) const {
     return static_cast<uint8_t*>(d) + m * ldd * (int64_t)sizeof(T);
+  }
+  __device__ __forceinline__ uint8_t* addr(int64_t m, int64_t n) const {
+    return row(m) + n * (int64_t)sizeof(T);
   }
 };
 
@@ -221,6 +227,31 @@ struct EpiRowColScaleT : EpiOut<uint16_t> {
 
 using EpiRowColScale = EpiRowColScaleT<false>;
 using EpiRowColScaleF16 = EpiRowColScaleT<true>;
+
+// H3 QKV scatter: the per-channel bf16 epilogue above, with column n of the
+// [M, 3 H D] product stored into the attention layout [1, H, M, D] of Q
+// (n < H D), K or V (reference nax_frag_store_dequant_cs_qkv,
+// _patches/int8_ext/int8_gemm.mm:445-474). D is a multiple of 8, so a
+// 16-byte store unit or a 4-column group never crosses a head.
+struct EpiRowColScaleQKV : EpiRowColScaleT<false> {
+  // K and V as byte offsets from Q (the output pointer d): the destination
+  // is then arithmetic in `kind`; a select among three pointers was turned
+  // into an indexed table in scratch memory by the compiler
+  int64_t koff, voff;
+  int64_t rows;              // M
+  uint32_t width, hd;        // H * D, D
+  __device__ __forceinline__ EpiRowColScaleQKV prepare() const { return *this; }
+  __device__ __forceinline__ uint8_t* addr(int64_t m, int64_t n) const {
+    const uint32_t nn = (uint32_t)n;
+    const uint32_t kind = nn / width, inner = nn - kind * width;
+    const uint32_t h = inner / hd, dd = inner - h * hd;
+    const int64_t off = koff * (int64_t)(kind == 1) + voff * (int64_t)(kind == 2);
+    return static_cast<uint8_t*>(this->d) + off + (((int64_t)h * rows + m) * hd + dd) * 2;
+  }
+  __device__ __forceinline__ uint2 value4(int64_t m, int64_t n, const int32_t (&v)[4], int nv) const {
+    return apply(rowp(m), col(n, nv), v);
+  }
+};
 
 // torch._scaled_mm on the fp8 route: out = f32 acc, then * scale_a,
 // * scale_b, * scale_result, + f32(bias), each in f32 and in this order,
@@ -431,7 +462,7 @@ struct EpiPairF : EpiOut<uint16_t> {
 template <class Epi, class Packed>
 __device__ __forceinline__ void store_group(const Epi& epi, int64_t m, int64_t n, int nv, Packed p) {
   using OutT = typename Epi::OutT;
-  uint8_t* dst = epi.row(m) + n * (int64_t)sizeof(OutT);
+  uint8_t* dst = epi.addr(m, n);
   if (epi.vec && nv == 4) {
     *reinterpret_cast<Packed*>(dst) = p;
     return;

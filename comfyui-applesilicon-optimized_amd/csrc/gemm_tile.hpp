@@ -484,7 +484,7 @@ __device__ __forceinline__ void store_unit(const Epi& epi, int64_t m, int64_t n,
                                            const Packed* p) {
   using OutT = typename Epi::OutT;
   if (epi.vec && nv >= 4 * GPU) {
-    uint8_t* dst = epi.row(m) + n * (int64_t)sizeof(OutT);
+    uint8_t* dst = epi.addr(m, n);
     if constexpr (sizeof(Packed) == 8 && GPU == 2)
       *reinterpret_cast<uint4*>(dst) = uint4{p[0].x, p[0].y, p[1].x, p[1].y};
     else

@@ -79,6 +79,33 @@ extern "C" int c4q_i8_gemm_nt_fused_cs_f16(const int8_t* a, int64_t lda, const i
                                  as_stream(stream), what);
 }
 
+extern "C" int c4q_i8_gemm_nt_fused_cs_qkv(const int8_t* a, int64_t lda, const int8_t* b,
+                                           int64_t ldb, uint16_t* q, uint16_t* k, uint16_t* v,
+                                           const float* row_scale, const float* col_scale,
+                                           const uint16_t* bias, int64_t M, int64_t K, int64_t H,
+                                           int64_t D, void* stream) {
+  const char* what = "c4q_i8_gemm_nt_fused_cs_qkv";
+  C4Q_REQUIRE(H > 0 && D > 0 && D % 8 == 0, C4Q_ERR_SHAPE,
+              "%s: need H > 0 and D > 0 a multiple of 8 (H=%lld D=%lld)", what, (long long)H,
+              (long long)D);
+  const int64_t N = 3 * H * D;
+  C4Q_REQUIRE(N < (1ll << 31) && M < (1ll << 31), C4Q_ERR_SHAPE, "%s: problem too large", what);
+  int st = check_i8_args(a, lda, b, ldb, q, N, M, N, K, what);
+  if (st) return st;
+  if (M == 0) return C4Q_OK;
+  C4Q_REQUIRE(k != nullptr && v != nullptr, C4Q_ERR_ARG, "%s: null K/V output", what);
+  C4Q_REQUIRE(row_scale != nullptr && col_scale != nullptr, C4Q_ERR_ARG,
+              "%s: null row_scale/col_scale", what);
+  const int vec = aligned16(q) && aligned16(k) && aligned16(v);
+  const int64_t koff = (int64_t)(reinterpret_cast<intptr_t>(k) - reinterpret_cast<intptr_t>(q));
+  const int64_t voff = (int64_t)(reinterpret_cast<intptr_t>(v) - reinterpret_cast<intptr_t>(q));
+  EpiRowColScaleQKV epi{{{q, N, vec}, row_scale, col_scale, bias}, koff, voff, M,
+                        (uint32_t)(H * D), (uint32_t)D};
+  return run_gemm8<OpI8T, GenI8>(reinterpret_cast<const uint8_t*>(a), lda,
+                                 reinterpret_cast<const uint8_t*>(b), ldb, M, N, K, epi,
+                                 as_stream(stream), what);
+}
+
 extern "C" int c4q_i8_ffn_pair(const int8_t* a, int64_t lda, const int8_t* w_gate,
                                const int8_t* w_up, int64_t ldw, uint16_t* d, int64_t ldd,
                                const float* row_scale, const float* gate_scale,

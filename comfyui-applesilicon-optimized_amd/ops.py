@@ -183,6 +183,34 @@ def i8_matmul2d_nt_fused_cs_half(a_i8, b_i8, row_scale, col_scale, bias=None):
     return d
 
 
+def i8_matmul2d_nt_fused_cs_qkv(a_i8, b_i8, row_scale, col_scale, bias, heads, head_dim,
+                                long_schedule=True):
+    """H3 QKV projection with the per-channel bf16 epilogue stored straight
+    into the attention layout: returns [Q, K, V], each [1, H, M, D] bf16
+    (_patches/int8_ext/int8_gemm.mm:2028-2110). long_schedule selects a
+    reference tile order that changes no output byte."""
+    del long_schedule
+    dev, lda, ldb = _i8_operands(a_i8, b_i8)
+    _req(a_i8.is_contiguous() and b_i8.is_contiguous(), "a/b must be contiguous 2D tensors")
+    M, K = a_i8.shape
+    N = b_i8.size(0)
+    _req(M > 64, "H3 QKV specialization requires M > 64")
+    H, D = int(heads), int(head_dim)
+    _req(H > 0 and D > 0 and N == 3 * H * D, "weight width must equal 3*H*D")
+    _req(D % 8 == 0, "head_dim must be a multiple of 8")
+    _dev(row_scale, col_scale, bias)
+    _vec(row_scale, M, torch.float32, "row_scale")
+    _vec(col_scale, N, torch.float32, "col_scale")
+    bias = _bias_bf16(bias, N)
+    outs = [torch.empty((1, H, M, D), dtype=torch.bfloat16, device=dev) for _ in range(3)]
+    with _on(dev):
+        _lib.call("c4q_i8_gemm_nt_fused_cs_qkv", a_i8.data_ptr(), lda, b_i8.data_ptr(), ldb,
+                  outs[0].data_ptr(), outs[1].data_ptr(), outs[2].data_ptr(),
+                  row_scale.data_ptr(), col_scale.data_ptr(),
+                  bias.data_ptr() if bias is not None else None, M, K, H, D, _stream(dev))
+    return outs
+
+
 def i8_merge_rot_quant(x, rotate=True):
     """x [B,H,S,D] bf16 (attention layout) -> (q [B*S, H*D] int8,
     scales [B*S, 1] fp32): head merge, ConvRot rotation of every 256-element

@@ -87,6 +87,17 @@ int c4q_i8_gemm_nt_fused_cs_f16(const int8_t* a, int64_t lda, const int8_t* b, i
                                 const float* col_scale, const uint16_t* bias,
                                 int64_t M, int64_t N, int64_t K, void* stream);
 
+/* H3 QKV variant: the c4q_i8_gemm_nt_fused_cs bf16 result [M, 3*H*D] stored
+ * straight into the attention layout: column n = kind*H*D + h*D + d goes to
+ * out_kind[((h * M) + m) * D + d], out_0/1/2 = q/k/v, each [1, H, M, D]
+ * contiguous. D must be a multiple of 8. Replaces i8_matmul2d_nt_fused_cs_qkv
+ * (_patches/int8_ext/int8_gemm.mm:2028-2110, epilogue :445-474) behind
+ * _int8_qkv_prequant (_patches/int8_linear_kernel_mps.py:266-360). */
+int c4q_i8_gemm_nt_fused_cs_qkv(const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb,
+                                uint16_t* q, uint16_t* k, uint16_t* v, const float* row_scale,
+                                const float* col_scale, const uint16_t* bias, int64_t M,
+                                int64_t K, int64_t H, int64_t D, void* stream);
+
 /* Rowwise int8 activation quant of x[M,K] (bf16 or f16):
  * q[M,K] int8 and scales[M] fp32, bit-exact with comfy_kitchen
  * quantize_int8_rowwise. Replaces i8_quant_rowwise

@@ -75,6 +75,15 @@ def epilogue_rowcolscale_half(c, row_scale, col_scale, bias_f16_bits=None):
     return d
 
 
+def scatter_qkv(d_bits, heads, head_dim):
+    """[M, 3 H D] -> (Q, K, V), each [1, H, M, D]: column kind*H*D + h*D + d
+    to out_kind[0, h, m, d] (reference ``int8_gemm.mm:466-471``)."""
+    d = np.asarray(d_bits)
+    m = d.shape[0]
+    x = d.reshape(m, 3, heads, head_dim).transpose(1, 2, 0, 3)
+    return [np.ascontiguousarray(x[k][None]) for k in range(3)]
+
+
 BF16_TINY = F32(2.0 ** -126)   # torch.finfo(torch.bfloat16).tiny
 F16_TINY = F32(2.0 ** -14)     # torch.finfo(torch.float16).tiny
 

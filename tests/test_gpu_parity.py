@@ -302,6 +302,27 @@ def test_moss_bf16_pair_generic_and_split_k(dev, monkeypatch):
     assert_bits_equal(bits16(out), ref, "moss bf16 pair split-K")
 
 
+@pytest.mark.parametrize("tile", [None, "5", "7"])
+@pytest.mark.parametrize("M,K,H,D", [(300, 1024, 4, 128), (77, 512, 3, 64), (1024, 3072, 24, 128)])
+def test_i8_fused_cs_qkv_exact(dev, monkeypatch, tile, M, K, H, D):
+    """H3 QKV scatter: the fused_cs bytes stored into [1, H, M, D] Q/K/V."""
+    if tile is not None:
+        monkeypatch.setenv("C4Q_TILE", tile)
+    g = gen(91 + M + H * D)
+    N = 3 * H * D
+    a, b = _randint8((M, K), g), _randint8((N, K), g)
+    rs = torch.rand(M, generator=g) * 0.01
+    cs = torch.rand(N, generator=g) * 0.02
+    bb = torch.randn(N, generator=g).to(torch.bfloat16)
+    outs = ops.i8_matmul2d_nt_fused_cs_qkv(a.to(dev), b.to(dev), rs.to(dev), cs.to(dev),
+                                           bb.to(dev), H, D)
+    ref = oi.scatter_qkv(oi.epilogue_rowcolscale(oi.i8_matmul2d_nt(a.numpy(), b.numpy()),
+                                                 rs.numpy(), cs.numpy(), bits16(bb)), H, D)
+    for name, o, r in zip("qkv", outs, ref):
+        assert o.shape == (1, H, M, D)
+        assert_bits_equal(bits16(o), r, f"qkv {name} {M}x{K} H{H} D{D} tile {tile}")
+
+
 def test_c1_golden_digest_full_size(dev):
     """BASELINE C1 at full size (seed 1): the kernel's INT32 product and
     per-channel bf16 epilogue hash to the digests written from torch._int_mm

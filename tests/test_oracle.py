@@ -464,3 +464,14 @@ def test_swiglu_rot_is_torch_swiglu_then_the_rotation():
     # gate and up swapped (a plausible mistake) differs
     xs = torch.cat([x[:, 512:], x[:, :512]], dim=1)
     assert not np.array_equal(ocr.swiglu_rot(tbits(xs), oact.silu_table()), got)
+
+
+def test_scatter_qkv_is_the_torch_split_and_head_transpose():
+    g = torch.Generator().manual_seed(45)
+    m, h, d = 5, 3, 8
+    y = torch.randn(m, 3 * h * d, generator=g).to(torch.bfloat16)
+    q, k, v = y.split(h * d, dim=1)
+    want = [t.reshape(m, h, d).transpose(0, 1).unsqueeze(0).contiguous() for t in (q, k, v)]
+    got = oi.scatter_qkv(tbits(y), h, d)
+    for a, b in zip(got, want):
+        assert np.array_equal(a, tbits(b))
