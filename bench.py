@@ -10,9 +10,11 @@ TFLOP/s (2*M*K*N per linear). ``roofline`` covers the dominant kernel of
 that step (the QKV W8A16 GEMM: one launch of whole rounds of 256x256 tiles
 plus one launch of the leftover tiles as split-K 64x64 pieces), timed with HIP
 events around each QKV call inside the timed region. ``per_config`` adds C1, C3, C4 and C5
-measured in the same process, plus MOSS_BF16, WAN_FP16 and CONVROT (the bf16
-FC1/SiTU pair, the fp16-output INT8 epilogue, the fused head-merge + ConvRot
-+ quant pass and the SwiGLU + ConvRot pass; not BASELINE configs); ``cpu_baseline`` times the reference's
+measured in the same process, plus MOSS_BF16, WAN_FP16, CONVROT and H3_QKV
+(the bf16 FC1/SiTU pair, the fp16-output INT8 epilogue, the fused head-merge
++ ConvRot + quant pass and the SwiGLU + ConvRot pass, the INT8 QKV projection
+into the attention layout with and without Q/K RMSNorm + RoPE; not BASELINE
+configs); ``cpu_baseline`` times the reference's
 PyTorch CPU path for C2 (kitchen dequant + bf16 F.linear) on a bounded row
 sample on this host's cores.
 
@@ -317,6 +319,48 @@ def bench_convrot(torch, ops, dev, steps, warmup):
     return res
 
 
+def bench_h3_qkv(torch, ops, dev, steps, warmup):
+    """H3 INT8 QKV projection (56 heads of 128, hidden 5376; 8192 tokens)
+    into the attention layout: the plain per-channel epilogue, the QKV
+    scatter, and the scatter + Q/K RMSNorm + partial RoPE (R = 48) on its
+    default route (scatter, then the in-place norm/RoPE pass) and on the
+    fused-epilogue route (C4Q_QKV_NORM_FUSE=1)."""
+    import os
+    M, H, K, R = 8192, 56, 5376, 48
+    N = 3 * H * 128
+    g = torch.Generator(device=dev).manual_seed(11)
+    a = torch.randint(-128, 128, (M, K), generator=g, device=dev, dtype=torch.int8)
+    b = torch.randint(-128, 128, (N, K), generator=g, device=dev, dtype=torch.int8)
+    rs = torch.rand(M, generator=g, device=dev) * 0.01
+    cs = torch.rand(N, generator=g, device=dev) * 0.002
+    bias = torch.randn(N, generator=g, device=dev).to(torch.bfloat16)
+    fr = torch.randn(M, R, 2, 2, generator=g, device=dev).to(torch.bfloat16)
+    qw = 1 + 0.1 * torch.randn(128, generator=g, device=dev)
+    kw = 1 + 0.1 * torch.randn(128, generator=g, device=dev)
+    ops_ = 2.0 * M * N * K
+    calls = {
+        "fused_cs": lambda: ops.i8_matmul2d_nt_fused_cs(a, b, rs, cs, bias),
+        "qkv_scatter": lambda: ops.i8_matmul2d_nt_fused_cs_qkv(a, b, rs, cs, bias, H, 128),
+        "qkv_rms_rope": lambda: ops.i8_matmul2d_nt_fused_cs_qkv_rms_rope(a, b, rs, cs, bias, fr, qw,
+                                                                        kw, H, 128, 1e-6),
+    }
+    res = {"shape": {"M": M, "K": K, "heads": H, "head_dim": 128, "rope_pairs": R}}
+    for name, fn in calls.items():
+        _, kern = Timer(torch).run(lambda p: marked(p, fn), max(5, steps // 2), max(2, warmup // 2))
+        res[name] = {"us": kern * 1e6, "tops": ops_ / kern / 1e12,
+                     "frac_int8_peak": ops_ / kern / 1e12 / PEAK["int8"]}
+    os.environ["C4Q_QKV_NORM_FUSE"] = "1"
+    try:
+        _, kern = Timer(torch).run(lambda p: marked(p, calls["qkv_rms_rope"]), max(5, steps // 2),
+                                   max(2, warmup // 2))
+    finally:
+        del os.environ["C4Q_QKV_NORM_FUSE"]
+    res["qkv_rms_rope_fused_epilogue"] = {"us": kern * 1e6, "tops": ops_ / kern / 1e12,
+                                          "frac_int8_peak": ops_ / kern / 1e12 / PEAK["int8"]}
+    return res
+
+
+# ----------------------------------------------------------------- C5 ---
 # ----------------------------------------------------------------- C5 ---
 
 def bench_c5(torch, ops, dev, steps, warmup):
@@ -459,9 +503,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--only", default="C1,C2,C3,C4,C5,MOSS_BF16,WAN_FP16,CONVROT",
+    ap.add_argument("--only", default="C1,C2,C3,C4,C5,MOSS_BF16,WAN_FP16,CONVROT,H3_QKV",
                     help="comma list of configs to run (C2 is always run); MOSS_BF16, "
-                         "WAN_FP16 and CONVROT time the widened rows (not BASELINE configs)")
+                         "WAN_FP16, CONVROT and H3_QKV time the widened rows (not BASELINE configs)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--pmc-target", action="store_true",
                     help="run the copy calibration and the C2 QKV kernel for rocprofv3 --pmc")
@@ -491,7 +535,7 @@ def main():
     torch.cuda.empty_cache()
     for name, fn in (("C1", bench_c1), ("C3", bench_c3), ("C4", bench_c4), ("C5", bench_c5),
                      ("MOSS_BF16", bench_moss_bf16), ("WAN_FP16", bench_wan_fp16),
-                     ("CONVROT", bench_convrot)):
+                     ("CONVROT", bench_convrot), ("H3_QKV", bench_h3_qkv)):
         if name in only:
             log(f"{name} ...")
             per[name] = fn(torch, ops, dev, args.steps, args.warmup)

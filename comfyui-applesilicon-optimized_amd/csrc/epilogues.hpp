@@ -253,6 +253,75 @@ struct EpiRowColScaleQKV : EpiRowColScaleT<false> {
   }
 };
 
+// bf16 rounding (nearest even) of an f32 value, as f32.
+__device__ __forceinline__ float round_bf16(float v) { return bf16lo(bf16x2_rne(v, v)); }
+
+// RMSNorm of one 128-element head row held by the 8 lanes 8p .. 8p+7 of a
+// wave: lane j holds x[k] = column 64 h + 8 j + k' (k = 8 h + k'). The squares
+// (exact in f32: x is a bf16 value) are summed per lane in k order, then over
+// the 8 lanes by xor partners 4, 2, 1 -- ((p0+p4)+(p2+p6)) + ((p1+p5)+(p3+p7))
+// on every lane; inv = 1 / sqrt(ss / 128 + eps) with correctly rounded sqrt
+// and division; y = bf16((x * inv) * w). Reference
+// _patches/int8_ext/int8_gemm.mm:806-833 (its sum order is Metal's simd_sum).
+// Sum of v over the 8 lanes 8p .. 8p+7 by xor partners 4, 2, 1, read
+// through DPP (row shifts by 4, quad permutes): every lane gets
+// ((v0+v4)+(v2+v6)) + ((v1+v5)+(v3+v7)). Needs all 64 lanes active.
+__device__ __forceinline__ float sum8_lanes(float v) {
+  const int iv = __builtin_bit_cast(int, v);
+  const int from_up = __builtin_amdgcn_update_dpp(0, iv, 0x104, 0xF, 0xF, true);   // row_shl:4
+  const int from_dn = __builtin_amdgcn_update_dpp(0, iv, 0x114, 0xF, 0xF, true);   // row_shr:4
+  v = v + __builtin_bit_cast(float, (threadIdx.x & 4) ? from_dn : from_up);
+  v = v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E,
+                                                                0xF, 0xF, true));  // lane ^ 2
+  v = v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1,
+                                                                0xF, 0xF, true));  // lane ^ 1
+  return v;
+}
+
+__device__ __forceinline__ void head_rms_norm(const float (&x)[16], const float (&w)[16], float eps,
+                                              float (&y)[16]) {
+  float ss = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) ss = ss + x[k] * x[k];
+  ss = sum8_lanes(ss);
+  const float inv = 1.0f / __builtin_sqrtf(ss * 0.0078125f + eps);
+#pragma unroll
+  for (int k = 0; k < 16; ++k) y[k] = round_bf16((x[k] * inv) * w[k]);
+}
+
+// Split-half RoPE of column d < 2R (reference int8_gemm.mm:843-854, the
+// eager `out = y * diag; out.addcmul_(y_partner, off)`): fw holds the bf16
+// pair freqs[m, d mod R, r, 0..1], r = (d >= R); the diagonal product is
+// rounded to bf16, the off-diagonal one (exact in f32) added with one
+// rounding.
+__device__ __forceinline__ float rope_split_half(float yd, float yp, uint32_t fw, bool second) {
+  const float f0 = bf16lo(fw), f1 = bf16hi(fw);
+  const float diag = second ? f1 : f0, off = second ? f0 : f1;
+  return round_bf16(round_bf16(diag * yd) + off * yp);
+}
+
+// H3 QKV projection with Q/K RMSNorm and partial split-half RoPE
+// (reference int8_matmul_fused_cs_qkv_rms_rope_impl,
+// _patches/int8_ext/int8_gemm.mm:683-861; host :2111-2209): the QKV
+// scatter above with D = 128. The tiled kernels run it with waves whose
+// sub-tile spans exactly one head (128 columns) and R a multiple of 8, see
+// epilogue_head_norm.
+struct EpiQKVNormRope : EpiRowColScaleQKV {
+  static constexpr bool kHeadNorm = true;
+  const uint32_t* freqs;    // [M, R, 2, 2] bf16, as [M, R, 2] pairs; 4-byte aligned
+  const float* qw;          // [128] f32 Q norm weight
+  int64_t kwoff;            // the K norm weight as a byte offset from qw
+  int32_t pairs;            // R, 2R <= 128
+  float eps;
+  __device__ __forceinline__ EpiQKVNormRope prepare() const { return *this; }
+  // norm weight of Q (kind 0) or K (kind 1): offset arithmetic, not a
+  // pointer select (see koff above)
+  __device__ __forceinline__ const float* weight(uint32_t kind) const {
+    return reinterpret_cast<const float*>(reinterpret_cast<const uint8_t*>(qw) +
+                                          kwoff * (int64_t)(kind == 1));
+  }
+};
+
 // torch._scaled_mm on the fp8 route: out = f32 acc, then * scale_a,
 // * scale_b, * scale_result, + f32(bias), each in f32 and in this order,
 // one final rounding to the output dtype

@@ -699,6 +699,165 @@ __device__ __forceinline__ void epilogue_pair(const Acc (&acc)[TM][TN], int64_t 
   }
 }
 
+// Epilogues that reduce over whole 128-column heads (EpiQKVNormRope).
+template <class E, class = void> struct IsHeadNorm : std::false_type {};
+template <class E>
+struct IsHeadNorm<E, std::void_t<decltype(E::kHeadNorm)>> : std::bool_constant<E::kHeadNorm> {};
+
+// Q/K RMSNorm + partial RoPE epilogue of a wave whose sub-tile spans one
+// head: 128 columns starting at n0, a multiple of 128, so the kind (Q, K or
+// V) and the head are the same for the whole sub-tile, and output row m of
+// it is the 256 contiguous bytes at hb + 256 m. R (rotation pairs) is a
+// multiple of 8 here, so each 8-column unit of a lane lies wholly in the
+// first rotated half (d < R), the second (R <= d < 2R) or the pass-through
+// part (d >= 2R): the per-element arithmetic is branch-free, with per-unit
+// constants set once per tile. Per strip of 8 rows:
+//   1. the accumulators pass through the strip as in epilogue_single; lane l
+//      forms the bf16 projection values of row l/8, columns c0 + k for its
+//      units c0 = 64 h + 8 (l%8), exactly the QKV scatter's values;
+//   2. V: stored as they are;
+//   3. Q, K: head_rms_norm over the 8 lanes of the row; the normalized
+//      values go back to the strip, each lane reads the 8 RoPE partners of
+//      each unit (columns c0 + R or c0 - R) and applies rope_split_half.
+// The row scale of the next strip is loaded one strip ahead, and with
+// AHEAD (a wave that has the register file of its SIMD to itself) the freqs
+// words as well; otherwise they load at the strip's RoPE step.
+template <int TM, int TN, bool AHEAD, class Acc, class Epi, class Params>
+__device__ __forceinline__ void epilogue_head_norm(const Acc (&acc)[TM][TN], int64_t m0, int64_t n0,
+                                                   int64_t M, int64_t N, const Epi& epi,
+                                                   uint8_t* lds, const Params& pr) {
+  static_assert(TN == 4, "head epilogue: a wave's sub-tile spans one 128-column head");
+  constexpr int COLS = TN * 32;
+  using Map = StoreMap<COLS, typename Epi::OutT>;
+  static_assert(Map::UNIT == 8 && Map::UPL == 2 && Map::GPU == 2, "head epilogue lane map");
+  using St = Strip<COLS>;
+  if (n0 >= N) return;                                   // wave-uniform: past the last head
+  int32_t* sw = reinterpret_cast<int32_t*>(lds);
+  float* sf = reinterpret_cast<float*>(lds);
+  const int lane = threadIdx.x & 63, prow = lane >> 3;
+  const uint32_t kind = (uint32_t)n0 / epi.width;        // 0 Q, 1 K, 2 V
+  uint8_t* const hb = epi.addr(0, n0);                   // row 0 of this head
+  const int R = epi.pairs;
+  // per unit h: its first column, where its partners start, the byte offset
+  // of its first freqs word in a freqs row, the half-swap of those words
+  // (second half: the diagonal factor is the high bf16), pass-through
+  int c0[2], pc[2], fo[2];
+  uint32_t swap[2];
+  bool pass[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    c0[h] = Map::col(lane, 2 * h);
+    const bool first = c0[h] < R, second = !first && c0[h] < 2 * R;
+    pass[h] = !first && !second;
+    pc[h] = first ? c0[h] + R : (second ? c0[h] - R : c0[h]);
+    fo[h] = first ? 8 * c0[h] : (second ? 8 * (c0[h] - R) + 4 : 0);
+    swap[h] = second ? 16u : 0u;
+  }
+  float w[16];
+  float rsv = epi.rowp(m0 + prow < M ? m0 + prow : M - 1);   // row scale, current strip
+  uint32_t fw[16];                                       // freqs words, current strip
+  // word k of unit h in freqs row m (clamped into [0, M)): freqs[m, i, r]
+  // for column c0 + k = i + r R
+  auto load_freqs = [&](int64_t m) __attribute__((always_inline)) {
+    const uint8_t* fr = reinterpret_cast<const uint8_t*>(epi.freqs) + (m < M ? m : M - 1) * R * 8;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      if (!pass[h]) {
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(fr + fo[h]);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) fw[8 * h + k] = p[2 * k];
+      }
+    }
+  };
+  if (kind < 2) {
+    const float* wp = epi.weight(kind);
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int k = 0; k < 8; k += 4) {
+        const float4 f = *reinterpret_cast<const float4*>(wp + c0[h] + k);
+        w[8 * h + k] = f.x; w[8 * h + k + 1] = f.y; w[8 * h + k + 2] = f.z; w[8 * h + k + 3] = f.w;
+      }
+    if constexpr (AHEAD) load_freqs(m0 + prow);
+  }
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          sw[St::word((lane >> 5) * 4 + r, j * 32 + (lane & 31))] = acc[i][j][4 * q + r];
+      lds_fence_wave();
+      const int64_t m = m0 + i * 32 + q * 8 + prow;
+      uint2 pv[4];                                        // group g = 2 h + gg: 4 columns
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int32_t* s = sw + St::word(prow, Map::col(lane, g));
+        const int32_t v[4] = {s[0], s[1], s[2], s[3]};
+        pv[g] = epi.apply(rsv, pr.col[g], v);
+      }
+      const bool more = i * 4 + q + 1 < TM * 4;
+      if (more) rsv = epi.rowp(m + 8 < M ? m + 8 : M - 1);
+      uint8_t* const dst = hb + m * 256;
+      if (kind == 2) {
+        if (m < M) {
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            *reinterpret_cast<uint4*>(dst + 2 * c0[h]) =
+                uint4{pv[2 * h].x, pv[2 * h].y, pv[2 * h + 1].x, pv[2 * h + 1].y};
+        }
+      } else {
+        float x[16], y[16];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          x[4 * g] = bf16lo(pv[g].x); x[4 * g + 1] = bf16hi(pv[g].x);
+          x[4 * g + 2] = bf16lo(pv[g].y); x[4 * g + 3] = bf16hi(pv[g].y);
+        }
+        head_rms_norm(x, w, epi.eps, y);
+        // each lane overwrites only the strip words it read itself
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int k = 0; k < 8; k += 4)
+            *reinterpret_cast<float4*>(sf + St::word(prow, c0[h] + k)) =
+                float4{y[8 * h + k], y[8 * h + k + 1], y[8 * h + k + 2], y[8 * h + k + 3]};
+        if constexpr (!AHEAD) load_freqs(m);
+        lds_fence_wave();
+        uint4 ov[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          float yp[8], o[8];
+#pragma unroll
+          for (int k = 0; k < 8; k += 4) {
+            const float4 t = *reinterpret_cast<const float4*>(sf + St::word(prow, pc[h] + k));
+            yp[k] = t.x; yp[k + 1] = t.y; yp[k + 2] = t.z; yp[k + 3] = t.w;
+          }
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            const uint32_t f = __builtin_amdgcn_alignbit(fw[8 * h + k], fw[8 * h + k], swap[h]);
+            const float r = rope_split_half(y[8 * h + k], yp[k], f, false);
+            o[k] = pass[h] ? y[8 * h + k] : r;
+          }
+          ov[h] = uint4{bf16x2_rne(o[0], o[1]), bf16x2_rne(o[2], o[3]), bf16x2_rne(o[4], o[5]),
+                        bf16x2_rne(o[6], o[7])};
+        }
+        // the next strip's freqs load under this strip's stores and the
+        // next strip's transpose and norm
+        if constexpr (AHEAD) {
+          if (more) load_freqs(m + 8);
+        }
+        if (m < M) {
+#pragma unroll
+          for (int h = 0; h < 2; ++h) *reinterpret_cast<uint4*>(dst + 2 * c0[h]) = ov[h];
+        }
+      }
+      lds_fence_wave();
+    }
+  }
+}
+
 // --------------------------------------------------------- main kernel ---
 
 // Operand sources: base pointers and strides; each workgroup derives its
@@ -881,6 +1040,8 @@ gemm_tile_kernel(GemmShape sh, Src2 sa, Src2 sb, const float* b_scale, Epi epi) 
     }
     if constexpr (PAIR) {
       epilogue_pair<TM, TN>(acc, wm0, wn0, sh.M, sh.N >> 1, ep, strip, prm);
+    } else if constexpr (IsHeadNorm<Epi>::value) {
+      epilogue_head_norm<TM, TN, (WM * WN <= 4)>(acc, wm0, wn0, sh.M, sh.N, ep, strip, prm);
     } else {
       epilogue_single<TM, TN>(acc, wm0, wn0, sh.M, sh.N, ep, strip, prm);
     }

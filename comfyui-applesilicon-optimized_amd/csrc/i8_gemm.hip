@@ -106,6 +106,141 @@ extern "C" int c4q_i8_gemm_nt_fused_cs_qkv(const int8_t* a, int64_t lda, const i
                                  as_stream(stream), what);
 }
 
+namespace {
+
+// In-place Q/K RMSNorm + partial RoPE over the attention layout [1, H, M,
+// 128] of Q and K: the pass after the QKV scatter where the fused epilogue
+// does not apply (R not a multiple of 8, or operands the tiled kernels
+// cannot take), with the lane map and arithmetic of epilogue_head_norm (8
+// rows per wave: lane l holds row l/8, columns 64 h + 8 (l%8) + k). Rows
+// run token-major -- row r is token m = r / 2H, kind (r / H) % 2, head r % H
+// -- so the 2H rows that share a token's freqs row run together. A row is
+// read whole before any lane writes it.
+__global__ void __launch_bounds__(256) head_norm_rope_kernel(EpiQKVNormRope epi, int64_t H) {
+  using St = Strip<128>;
+  using Map = StoreMap<128, uint16_t>;
+  __shared__ float rows[4][St::kBytes / 4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, prow = lane >> 3;
+  const int64_t r = ((int64_t)blockIdx.x * 4 + wave) * 8 + prow;
+  const bool live = r < 2 * H * epi.rows;
+  const int64_t m = r / (2 * H), t = r - m * 2 * H;
+  const uint32_t kind = t >= H ? 1u : 0u;
+  const int64_t hd = t - (int64_t)kind * H;
+  uint8_t* row = static_cast<uint8_t*>(epi.d) + epi.koff * (int64_t)kind + (hd * epi.rows + m) * 256;
+  const float* wp = epi.weight(kind);
+  float x[16], w[16], y[16];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int c = Map::col(lane, 2 * h);
+    uint4 u{0, 0, 0, 0};
+    if (live) u = *reinterpret_cast<const uint4*>(row + c * 2);
+    const uint32_t p[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[8 * h + 2 * e] = bf16lo(p[e]);
+      x[8 * h + 2 * e + 1] = bf16hi(p[e]);
+    }
+#pragma unroll
+    for (int k = 0; k < 8; k += 4) {
+      const float4 f = *reinterpret_cast<const float4*>(wp + c + k);
+      w[8 * h + k] = f.x; w[8 * h + k + 1] = f.y; w[8 * h + k + 2] = f.z; w[8 * h + k + 3] = f.w;
+    }
+  }
+  head_rms_norm(x, w, epi.eps, y);
+  float* sf = rows[wave];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int k = 0; k < 8; ++k) sf[St::word(prow, Map::col(lane, 2 * h) + k)] = y[8 * h + k];
+  lds_fence_wave();
+  if (!live) return;
+  const int R = epi.pairs;
+  const uint32_t* fr = epi.freqs + m * R * 2;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int c0 = Map::col(lane, 2 * h);
+    float o[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int d = c0 + k;
+      o[k] = y[8 * h + k];
+      if (d < 2 * R) {
+        const bool second = d >= R;
+        const int ii = second ? d - R : d;
+        const float yp = sf[St::word(prow, second ? ii : d + R)];
+        o[k] = rope_split_half(o[k], yp, fr[2 * ii + (second ? 1 : 0)], second);
+      }
+    }
+    *reinterpret_cast<uint4*>(row + c0 * 2) =
+        uint4{bf16x2_rne(o[0], o[1]), bf16x2_rne(o[2], o[3]), bf16x2_rne(o[4], o[5]),
+              bf16x2_rne(o[6], o[7])};
+  }
+}
+
+}  // namespace
+
+extern "C" int c4q_i8_gemm_nt_fused_cs_qkv_rms_rope(
+    const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb, uint16_t* q, uint16_t* k,
+    uint16_t* v, const float* row_scale, const float* col_scale, const uint16_t* bias,
+    const uint16_t* freqs, const float* q_weight, const float* k_weight, int64_t M, int64_t K,
+    int64_t H, int64_t R, float eps, void* stream) {
+  const char* what = "c4q_i8_gemm_nt_fused_cs_qkv_rms_rope";
+  constexpr int64_t D = 128;
+  C4Q_REQUIRE(H > 0 && R >= 0 && 2 * R <= D, C4Q_ERR_SHAPE,
+              "%s: need H > 0 and 0 <= 2R <= 128 (H=%lld R=%lld)", what, (long long)H,
+              (long long)R);
+  const int64_t N = 3 * H * D;
+  C4Q_REQUIRE(N < (1ll << 31) && M < (1ll << 31), C4Q_ERR_SHAPE, "%s: problem too large", what);
+  int st = check_i8_args(a, lda, b, ldb, q, N, M, N, K, what);
+  if (st) return st;
+  if (M == 0) return C4Q_OK;
+  C4Q_REQUIRE(k != nullptr && v != nullptr, C4Q_ERR_ARG, "%s: null K/V output", what);
+  C4Q_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v), C4Q_ERR_ARG,
+              "%s: Q, K and V must be 16-byte aligned", what);
+  C4Q_REQUIRE(row_scale != nullptr && col_scale != nullptr, C4Q_ERR_ARG,
+              "%s: null row_scale/col_scale", what);
+  C4Q_REQUIRE(q_weight != nullptr && k_weight != nullptr && aligned16(q_weight) &&
+                  aligned16(k_weight),
+              C4Q_ERR_ARG, "%s: q_weight/k_weight must be non-null and 16-byte aligned", what);
+  C4Q_REQUIRE(R == 0 || (freqs != nullptr && (reinterpret_cast<uintptr_t>(freqs) & 3u) == 0),
+              C4Q_ERR_ARG, "%s: freqs must be non-null and 4-byte aligned", what);
+  const int64_t koff = (int64_t)(reinterpret_cast<intptr_t>(k) - reinterpret_cast<intptr_t>(q));
+  const int64_t voff = (int64_t)(reinterpret_cast<intptr_t>(v) - reinterpret_cast<intptr_t>(q));
+  const int64_t kwoff =
+      (int64_t)(reinterpret_cast<intptr_t>(k_weight) - reinterpret_cast<intptr_t>(q_weight));
+  EpiQKVNormRope epi{{{{q, N, 1}, row_scale, col_scale, bias}, koff, voff, M, (uint32_t)(H * D),
+                      (uint32_t)D},
+                     reinterpret_cast<const uint32_t*>(freqs), q_weight, kwoff, (int32_t)R, eps};
+  hipStream_t s = as_stream(stream);
+  const uint8_t* a8 = reinterpret_cast<const uint8_t*>(a);
+  const uint8_t* b8 = reinterpret_cast<const uint8_t*>(b);
+  const bool tiled = K > 0 && K % 16 == 0 && aligned16(a) && aligned16(b) && lda % 16 == 0 &&
+                     ldb % 16 == 0 && tile_offsets_fit(lda, ldb);
+  const Src2 sa{a8, a8, lda, M}, sb{b8, b8, ldb, N};
+  auto op_for = [](auto t) { return OpI8T<decltype(t)::KS8>{}; };
+  // Two routes, identical bytes. Fused: the projection with the norm/RoPE
+  // epilogue (whole 8-column units per rotation half, so R % 8 == 0). Two
+  // passes: the QKV scatter (the general 8-wave tiles), then the in-place
+  // norm/RoPE pass over Q and K, which mostly re-reads them from the
+  // Infinity Cache. On MI355X the second is the faster at H3's shapes
+  // (56 heads, K 5376: 1020 vs 1113 us at 8192 tokens, 726 vs 775 at 5378,
+  // 2121 vs 2085 at 17000), the norm epilogue's VALU work being exposed in
+  // the fused kernel; C4Q_QKV_NORM_FUSE=1 selects the fused route.
+  const char* fuse_env = getenv("C4Q_QKV_NORM_FUSE");
+  const bool fuse = fuse_env && fuse_env[0] == '1' && fuse_env[1] == 0;
+  if (tiled && R % 8 == 0 && fuse)
+    return run_tiles<false>(M, N, N, K, sa, sb, nullptr, epi, s, what, op_for, HeadTiles{});
+  // the QKV scatter, then the norm/RoPE pass over Q and K in place
+  const EpiRowColScaleQKV& scatter = epi;
+  st = tiled ? run_tiles<false>(M, N, N, K, sa, sb, nullptr, scatter, s, what, op_for)
+             : launch_generic(M, N, K, GenI8::make(a8, lda, b8, ldb), scatter, s, what);
+  if (st) return st;
+  const int64_t blocks = cdiv(2 * H * M, 32);
+  C4Q_REQUIRE(blocks < (1ll << 31), C4Q_ERR_SHAPE, "%s: problem too large", what);
+  hipLaunchKernelGGL(head_norm_rope_kernel, dim3((unsigned)blocks), dim3(256), 0, s, epi, H);
+  return check_launch(what);
+}
+
 extern "C" int c4q_i8_ffn_pair(const int8_t* a, int64_t lda, const int8_t* w_gate,
                                const int8_t* w_up, int64_t ldw, uint16_t* d, int64_t ldd,
                                const float* row_scale, const float* gate_scale,

@@ -152,24 +152,19 @@ inline int tile_bn(int id) { return with_tile(id, [](auto t) { return decltype(t
 // leftover pieces: as the only tile of a GEMM it loses to 64x128.
 // A tile id in the environment variable C4Q_TILE (0..7) forces one launch
 // of that variant, for tuning sweeps.
-inline TilePlan plan_tiles(int64_t M, int64_t N, int64_t K, int cus) {
-  const char* env = getenv("C4Q_TILE");
-  if (env && env[0] >= '0' && env[0] < '0' + TILE_COUNT && env[1] == 0) {
-    const int id = env[0] - '0';
-    return {id, cdiv(M, tile_bm(id)) * cdiv(N, tile_bn(id)), -1};
-  }
-  struct Cand { int id, per_cu; double eff; };
-  static const Cand cands[] = {{TILE_256x256_W8, 1, 1.00},
-                               {TILE_128x128_W4_K128, 2, 0.87},
-                               {TILE_64x128_W4_K128, 2, 0.70}};
-  static const Cand tails[] = {{TILE_128x128_W4_K128, 2, 0.87},
-                               {TILE_64x128_W4_K128, 2, 0.70},
-                               {TILE_64x64_KG4, 1, 0.30}};
+struct TileCand { int id, per_cu; double eff; };
+
+// The cost model over a list of main tiles and a list of tail tiles; bm_of
+// and bn_of give a tile id's shape.
+inline TilePlan plan_from(const TileCand* cands, int nc, const TileCand* tails, int nt,
+                          int (*bm_of)(int), int (*bn_of)(int), int64_t M, int64_t N, int64_t K,
+                          int cus) {
   const double gap = 9e6 / (double)(K > 0 ? K : 1);
-  TilePlan best{TILE_256x256_W8, 0, -1};
+  TilePlan best{cands[0].id, 0, -1};
   double best_cost = -1;
-  for (const Cand& c : cands) {
-    const int bm = tile_bm(c.id), bn = tile_bn(c.id);
+  for (int ci = 0; ci < nc; ++ci) {
+    const TileCand& c = cands[ci];
+    const int bm = bm_of(c.id), bn = bn_of(c.id);
     const int64_t tiles = cdiv(M, bm) * cdiv(N, bn);
     const int64_t slots = (int64_t)cus * c.per_cu;
     const double round = (double)c.per_cu * bm * bn / c.eff;
@@ -180,8 +175,9 @@ inline TilePlan plan_tiles(int64_t M, int64_t N, int64_t K, int cus) {
     }
     const int64_t whole = tiles / slots * slots, rest = tiles - whole;
     if (whole == 0 || rest == 0) continue;
-    for (const Cand& t : tails) {
-      const int tm = tile_bm(t.id), tn = tile_bn(t.id);
+    for (int ti = 0; ti < nt; ++ti) {
+      const TileCand& t = tails[ti];
+      const int tm = bm_of(t.id), tn = bn_of(t.id);
       if (tm * tn >= bm * bn || bm % tm || bn % tn) continue;
       const int64_t pieces = rest * (bm / tm) * (bn / tn);
       const int64_t tslots = (int64_t)cus * t.per_cu;
@@ -196,13 +192,73 @@ inline TilePlan plan_tiles(int64_t M, int64_t N, int64_t K, int cus) {
   return best;
 }
 
+// A tile id forced by the environment variable `name` (one digit below
+// `count`), else -1.
+inline int forced_tile(const char* name, int count) {
+  const char* env = getenv(name);
+  if (env && env[0] >= '0' && env[0] < '0' + count && env[1] == 0) return env[0] - '0';
+  return -1;
+}
+
+inline TilePlan plan_tiles(int64_t M, int64_t N, int64_t K, int cus) {
+  const int id = forced_tile("C4Q_TILE", TILE_COUNT);
+  if (id >= 0) return {id, cdiv(M, tile_bm(id)) * cdiv(N, tile_bn(id)), -1};
+  static const TileCand cands[] = {{TILE_256x256_W8, 1, 1.00},
+                                   {TILE_128x128_W4_K128, 2, 0.87},
+                                   {TILE_64x128_W4_K128, 2, 0.70}};
+  static const TileCand tails[] = {{TILE_128x128_W4_K128, 2, 0.87},
+                                   {TILE_64x128_W4_K128, 2, 0.70},
+                                   {TILE_64x64_KG4, 1, 0.30}};
+  return plan_from(cands, 3, tails, 3, tile_bm, tile_bn, M, N, K, cus);
+}
+
+// The tile set of the general kernels.
+struct MainTiles {
+  template <class F> static int with(int id, F&& f) { return with_tile(id, f); }
+  static int bm(int id) { return tile_bm(id); }
+  static int bn(int id) { return tile_bn(id); }
+  static TilePlan plan(int64_t M, int64_t N, int64_t K, int cus) { return plan_tiles(M, N, K, cus); }
+};
+
+// Tiles whose waves each span 128 output columns -- one attention head --
+// for epilogues that reduce over a head (IsHeadNorm): 256x256 with 8 waves
+// of 64x128 (4 x 2; two waves per SIMD, so one wave's epilogue latency
+// hides behind the other's work), 128x128 with 2 waves of 64x128 (two
+// workgroups per CU) for leftover tiles, and 256x256 with 4 waves of
+// 128x128. C4Q_HEAD_TILE=0/1/2 forces one launch of one of them, for
+// tuning sweeps.
+enum HeadTileId : int {
+  HEAD_TILE_256x256_W8 = 0,
+  HEAD_TILE_128x128_W2 = 1,
+  HEAD_TILE_256x256_W4 = 2,
+  HEAD_TILE_COUNT = 3
+};
+struct HeadTiles {
+  template <class F> static int with(int id, F&& f) {
+    if (id == HEAD_TILE_256x256_W8) return f(Tile<256, 256, 4, 2, 160, 128>{});
+    if (id == HEAD_TILE_256x256_W4) return f(Tile<256, 256, 2, 2, 160, 128>{});
+    return f(Tile<128, 128, 2, 1, 80, 128>{});
+  }
+  static int bm(int id) { return id == HEAD_TILE_128x128_W2 ? 128 : 256; }
+  static int bn(int id) { return id == HEAD_TILE_128x128_W2 ? 128 : 256; }
+  static TilePlan plan(int64_t M, int64_t N, int64_t K, int cus) {
+    const int id = forced_tile("C4Q_HEAD_TILE", HEAD_TILE_COUNT);
+    if (id >= 0) return {id, cdiv(M, bm(id)) * cdiv(N, bn(id)), -1};
+    static const TileCand cands[] = {{HEAD_TILE_256x256_W8, 1, 1.00},
+                                     {HEAD_TILE_128x128_W2, 2, 0.70}};
+    static const TileCand tails[] = {{HEAD_TILE_128x128_W2, 2, 0.70}};
+    return plan_from(cands, 2, tails, 1, bm, bn, M, N, K, cus);
+  }
+};
+
 // The launches of a GEMM's tile plan as (tile id, shape) pairs; returns
 // their number (1 or 2). n_rows_b = rows of the B tile space (pair kernels:
 // 2 * N_out), N = output columns.
+template <class Set = MainTiles>
 inline int plan_launches(int64_t M, int64_t n_rows_b, int64_t N, int64_t K, int cus, int ids[2],
                          GemmShape shs[2]) {
-  const TilePlan p = plan_tiles(M, n_rows_b, K, cus);
-  const int bm = tile_bm(p.main_id), bn = tile_bn(p.main_id);
+  const TilePlan p = Set::plan(M, n_rows_b, K, cus);
+  const int bm = Set::bm(p.main_id), bn = Set::bn(p.main_id);
   const int64_t mapped = cdiv(M, bm) * cdiv(n_rows_b, bn);
   GemmShape sh{M, N, K, (int)cdiv(M, bm), (int)cdiv(n_rows_b, bn), 0, (int)p.main_count, 1, 1};
   int n = 0;
@@ -212,8 +268,8 @@ inline int plan_launches(int64_t M, int64_t n_rows_b, int64_t N, int64_t K, int 
   }
   if (p.tail_id >= 0) {
     sh.first = (int)p.main_count;
-    sh.sub_m = bm / tile_bm(p.tail_id);
-    sh.sub_n = bn / tile_bn(p.tail_id);
+    sh.sub_m = bm / Set::bm(p.tail_id);
+    sh.sub_n = bn / Set::bn(p.tail_id);
     sh.count = (int)((mapped - p.main_count) * sh.sub_m * sh.sub_n);
     ids[n] = p.tail_id;
     shs[n++] = sh;
@@ -223,17 +279,18 @@ inline int plan_launches(int64_t M, int64_t n_rows_b, int64_t N, int64_t K, int 
 
 // Runs a GEMM through its tile plan. OpFor maps a Tile to its operand policy
 // (a callable whose return type is the policy).
-template <bool PAIR, class OpFor, class Epi>
+template <bool PAIR, class OpFor, class Epi, class Set = MainTiles>
 int run_tiles(int64_t M, int64_t n_rows_b, int64_t N, int64_t K, const Src2& sa, const Src2& sb,
-              const float* b_scale, const Epi& epi, hipStream_t s, const char* what, OpFor op_for) {
+              const float* b_scale, const Epi& epi, hipStream_t s, const char* what, OpFor op_for,
+              Set = {}) {
   // bound on the tile count of any plan (the smallest tile is 64 x 64)
   C4Q_REQUIRE(cdiv(M, 64) * cdiv(n_rows_b, 64) < (1ll << 27), C4Q_ERR_SHAPE,
               "%s: problem too large (%lld x %lld)", what, (long long)M, (long long)n_rows_b);
   int ids[2];
   GemmShape shs[2];
-  const int n = plan_launches(M, n_rows_b, N, K, device_cus(), ids, shs);
+  const int n = plan_launches<Set>(M, n_rows_b, N, K, device_cus(), ids, shs);
   for (int l = 0; l < n; ++l) {
-    const int st = with_tile(ids[l], [&](auto t) {
+    const int st = Set::with(ids[l], [&](auto t) {
       using T = decltype(t);
       return launch_tile<T, decltype(op_for(t)), PAIR>(shs[l], sa, sb, b_scale, epi, s, what);
     });

@@ -211,6 +211,50 @@ def i8_matmul2d_nt_fused_cs_qkv(a_i8, b_i8, row_scale, col_scale, bias, heads, h
     return outs
 
 
+def i8_matmul2d_nt_fused_cs_qkv_rms_rope(a_i8, b_i8, row_scale, col_scale, bias, freqs,
+                                         q_weight, k_weight, heads, head_dim, eps,
+                                         long_schedule=True):
+    """H3 QKV projection whose Q and K heads get RMSNorm (fp32 weights
+    q_weight / k_weight, eps) and partial split-half RoPE (freqs bf16
+    [..., M, R, 2, 2], rotating the first 2R of D = 128 columns) before the
+    store; returns [Q, K, V], each [1, H, M, 128] bf16
+    (_patches/int8_ext/int8_gemm.mm:2111-2209, kernel :683-861).
+    long_schedule selects a reference tile order that changes no output
+    byte."""
+    del long_schedule
+    dev, lda, ldb = _i8_operands(a_i8, b_i8)
+    _req(a_i8.is_contiguous() and b_i8.is_contiguous(), "a/b must be contiguous 2D tensors")
+    M, K = a_i8.shape
+    N = b_i8.size(0)
+    _req(M > 64, "H3 QKV specialization requires M > 64")
+    H, D = int(heads), int(head_dim)
+    _req(H > 0 and D == 128 and N == 3 * H * D,
+         "fused QKV norm/RoPE requires D=128 and width=3*H*D")
+    _dev(row_scale, col_scale, bias, freqs, q_weight, k_weight)
+    _vec(row_scale, M, torch.float32, "row_scale")
+    _vec(col_scale, N, torch.float32, "col_scale")
+    _req(freqs.dtype == torch.bfloat16 and freqs.is_contiguous() and freqs.dim() >= 3,
+         "freqs must be contiguous bf16")
+    R = int(freqs.size(-3))
+    _req(R > 0 and 2 * R <= D and freqs.numel() == M * R * 4, "freqs shape mismatch")
+    for name, w in (("q_weight", q_weight), ("k_weight", k_weight)):
+        _req(w.dtype == torch.float32 and w.is_contiguous() and w.numel() == D,
+             f"{name} must be {D} contiguous float32 elements")
+    # the kernels read the weights 16 bytes and the freqs 4 bytes at a time
+    q_weight, k_weight = (w if w.data_ptr() % 16 == 0 else w.clone() for w in (q_weight, k_weight))
+    if freqs.data_ptr() % 4:
+        freqs = freqs.clone()
+    bias = _bias_bf16(bias, N)
+    outs = [torch.empty((1, H, M, D), dtype=torch.bfloat16, device=dev) for _ in range(3)]
+    with _on(dev):
+        _lib.call("c4q_i8_gemm_nt_fused_cs_qkv_rms_rope", a_i8.data_ptr(), lda, b_i8.data_ptr(),
+                  ldb, outs[0].data_ptr(), outs[1].data_ptr(), outs[2].data_ptr(),
+                  row_scale.data_ptr(), col_scale.data_ptr(),
+                  bias.data_ptr() if bias is not None else None, freqs.data_ptr(),
+                  q_weight.data_ptr(), k_weight.data_ptr(), M, K, H, R, float(eps), _stream(dev))
+    return outs
+
+
 def i8_merge_rot_quant(x, rotate=True):
     """x [B,H,S,D] bf16 (attention layout) -> (q [B*S, H*D] int8,
     scales [B*S, 1] fp32): head merge, ConvRot rotation of every 256-element

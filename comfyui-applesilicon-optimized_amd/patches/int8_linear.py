@@ -162,6 +162,69 @@ def _plain_int8_layer(layer):
     return w
 
 
+def _int8_qkv_prequant(layer, x, heads, head_dim, norm_rope):
+    """The H3 QKV projection straight into the attention layout (reference
+    ``_int8_qkv_prequant``, ``:266-412``): [Q, K, V], each [1, H, S, D]
+    bf16, or None when a check fails (the caller then runs the layer and
+    splits heads itself). ``norm_rope`` is None (layout only) or
+    (freqs, q_weight, k_weight, eps) for the D = 128 RMSNorm + partial RoPE
+    epilogue. Runtime LoRA adapters and ConvRot weights are not served
+    (None). Switches: ``C4Q_INT8_QKV_SCATTER=0`` / ``C4Q_INT8_QKV_NORM_ROPE=0``
+    (or the reference's ``ASFP8_`` names)."""
+    def _on(name):
+        return os.environ.get("C4Q_" + name, os.environ.get("ASFP8_" + name, "1")) == "1"
+
+    if not _on("INT8_QKV_SCATTER") or (norm_rope is not None and not _on("INT8_QKV_NORM_ROPE")):
+        return None
+    if getattr(layer, "_asfp8_runtime_lora", None) is not None:
+        return None
+    if (not isinstance(x, torch.Tensor) or x.dim() != 2 or not _common.on_device(x)
+            or x.dtype != torch.bfloat16 or not x.is_contiguous()):
+        return None
+    w = _plain_int8_layer(layer)
+    if w is None:
+        return None
+    params = w._params
+    if getattr(params, "convrot", False):
+        return None
+    qdata = w._qdata
+    if tuple(qdata.shape) != (3 * heads * head_dim, x.shape[1]):
+        return None
+    weight_scale = params.scale.reshape(-1)
+    if weight_scale.numel() != qdata.shape[0]:
+        return None
+    try:
+        x_8, x_scale = _quant_cached(x)
+        bias = layer.bias
+        bias_arg = bias.to(torch.bfloat16) if bias is not None else None
+        common = (x_8, qdata.contiguous(), x_scale.reshape(-1).float().contiguous(),
+                  weight_scale.float().contiguous(), bias_arg)
+        if norm_rope is None:
+            return ops.i8_matmul2d_nt_fused_cs_qkv(*common, heads, head_dim)
+        freqs, q_weight, k_weight, eps = norm_rope
+        if (not isinstance(freqs, torch.Tensor) or not isinstance(q_weight, torch.Tensor)
+                or not isinstance(k_weight, torch.Tensor)):
+            return None
+        return ops.i8_matmul2d_nt_fused_cs_qkv_rms_rope(*common, freqs, q_weight, k_weight,
+                                                        heads, head_dim, float(eps))
+    except C4QError as e:
+        route = "qkv norm/RoPE epilogue" if norm_rope is not None else "qkv scatter"
+        print(f"{TAG} {route} fell back ({e})")
+        return None
+
+
+def int8_qkv_prequant(layer, x, heads, head_dim):
+    """H3 QKV projection directly to contiguous [1, H, S, D] Q/K/V
+    (reference ``:414-420``)."""
+    return _int8_qkv_prequant(layer, x, heads, head_dim, None)
+
+
+def int8_qkv_rms_rope_prequant(layer, x, freqs, q_weight, k_weight, heads, head_dim, eps):
+    """H3 INT8 projection + Q/K RMSNorm / partial-RoPE epilogue (reference
+    ``:423-432``)."""
+    return _int8_qkv_prequant(layer, x, heads, head_dim, (freqs, q_weight, k_weight, eps))
+
+
 def int8_o_proj_prequant(layer, out_bhsd):
     """o-projection straight from the attention layout [B, H, S, D]
     (reference ``:436-535``): bf16 [B, S, N], or None when a check fails

@@ -98,6 +98,24 @@ int c4q_i8_gemm_nt_fused_cs_qkv(const int8_t* a, int64_t lda, const int8_t* b, i
                                 const float* col_scale, const uint16_t* bias, int64_t M,
                                 int64_t K, int64_t H, int64_t D, void* stream);
 
+/* H3 QKV + Q/K RMSNorm + partial split-half RoPE, D = 128: the QKV variant
+ * above, with each Q and K head row x (bf16 projection values) stored as
+ *   inv = 1/sqrt(sum(x^2)/128 + eps), y = bf16((x*inv)*w)  w: q_weight/k_weight f32[128]
+ *   d < 2R: bf16(bf16(f[r]*y_d) + f[1-r]*y_partner), f = freqs[m, d mod R, r, 0..1],
+ *           r = (d >= R), partner = d+R or d-R;  d >= 2R: y_d
+ * and V stored unchanged. freqs: bf16 [M, R, 2, 2], 4-byte aligned (may be
+ * NULL when R = 0); 0 <= 2R <= 128. Q, K, V and the weights 16-byte
+ * aligned. Replaces i8_matmul2d_nt_fused_cs_qkv_rms_rope
+ * (_patches/int8_ext/int8_gemm.mm:2111-2209, kernel :683-861) behind
+ * int8_qkv_rms_rope_prequant (_patches/int8_linear_kernel_mps.py:423-432). */
+int c4q_i8_gemm_nt_fused_cs_qkv_rms_rope(const int8_t* a, int64_t lda, const int8_t* b,
+                                         int64_t ldb, uint16_t* q, uint16_t* k, uint16_t* v,
+                                         const float* row_scale, const float* col_scale,
+                                         const uint16_t* bias, const uint16_t* freqs,
+                                         const float* q_weight, const float* k_weight,
+                                         int64_t M, int64_t K, int64_t H, int64_t R, float eps,
+                                         void* stream);
+
 /* Rowwise int8 activation quant of x[M,K] (bf16 or f16):
  * q[M,K] int8 and scales[M] fp32, bit-exact with comfy_kitchen
  * quantize_int8_rowwise. Replaces i8_quant_rowwise

@@ -95,18 +95,19 @@ extern "C" int c4q_probe_div_bf16_exhaustive(unsigned long long* out, void* stre
 // multiple of the cell). info[8]: launches, then (tile id, kernel tiles) of
 // each launch, then the main launch's first and the tail launch's sub_m,
 // sub_n. Returns 0, or -1 if cover_len is too small.
-extern "C" int c4q_probe_tile_plan(int64_t M, int64_t n_rows_b, int64_t K, int cus, int32_t* cover,
-                                   int64_t cover_len, int64_t* info) {
+template <class Set>
+static int probe_plan(int64_t M, int64_t n_rows_b, int64_t K, int cus, int32_t* cover,
+                      int64_t cover_len, int64_t* info) {
   const int64_t cm = cdiv(M, 64), cn = cdiv(n_rows_b, 64);
   if (cm * cn > cover_len) return -1;
   for (int64_t i = 0; i < cm * cn; ++i) cover[i] = 0;
   int ids[2];
   GemmShape shs[2];
-  const int n = plan_launches(M, n_rows_b, n_rows_b, K, cus, ids, shs);
+  const int n = plan_launches<Set>(M, n_rows_b, n_rows_b, K, cus, ids, shs);
   for (int k = 0; k < 8; ++k) info[k] = 0;
   info[0] = n;
   for (int l = 0; l < n; ++l) {
-    const int bm = tile_bm(ids[l]), bn = tile_bn(ids[l]);
+    const int bm = Set::bm(ids[l]), bn = Set::bn(ids[l]);
     info[1 + 2 * l] = ids[l];
     info[2 + 2 * l] = shs[l].count;
     if (l == 1) {
@@ -122,4 +123,16 @@ extern "C" int c4q_probe_tile_plan(int64_t M, int64_t n_rows_b, int64_t K, int c
   }
   info[5] = n ? shs[0].first : 0;
   return 0;
+}
+
+extern "C" int c4q_probe_tile_plan(int64_t M, int64_t n_rows_b, int64_t K, int cus, int32_t* cover,
+                                   int64_t cover_len, int64_t* info) {
+  return probe_plan<MainTiles>(M, n_rows_b, K, cus, cover, cover_len, info);
+}
+
+// The same for the head-spanning tile set (HeadTiles: ids 0 = 256x256 with
+// 4 waves, 1 = 128x128 with 2 waves).
+extern "C" int c4q_probe_head_tile_plan(int64_t M, int64_t n_rows_b, int64_t K, int cus,
+                                        int32_t* cover, int64_t cover_len, int64_t* info) {
+  return probe_plan<HeadTiles>(M, n_rows_b, K, cus, cover, cover_len, info);
 }

@@ -15,9 +15,11 @@ from oracle import convrot as ocr
 from oracle import fp8 as of
 from oracle import int8 as oi
 from oracle import pair as op
+from oracle import qknorm as oqk
 from oracle.numerics import bf16_bits_to_f32, f16_bits_to_f32
 
 import cdna4q.ops as ops
+from cdna4q._lib import C4QError
 
 pytestmark = pytest.mark.gpu
 
@@ -321,6 +323,92 @@ def test_i8_fused_cs_qkv_exact(dev, monkeypatch, tile, M, K, H, D):
     for name, o, r in zip("qkv", outs, ref):
         assert o.shape == (1, H, M, D)
         assert_bits_equal(bits16(o), r, f"qkv {name} {M}x{K} H{H} D{D} tile {tile}")
+
+
+def _qkv_rope_case(M, K, H, R, seed, unaligned=False):
+    g = gen(seed)
+    N = 3 * H * 128
+    a, b = _randint8((M, K), g), _randint8((N, K), g)
+    rs = torch.rand(M, generator=g) * 0.01
+    cs = torch.rand(N, generator=g) * 0.02
+    bb = torch.randn(N, generator=g).to(torch.bfloat16)
+    freqs = torch.randn(1, M, 1, R, 2, 2, generator=g).to(torch.bfloat16)
+    qw = (1 + torch.randn(128, generator=g) * 0.1).float()
+    kw = (1 + torch.randn(128, generator=g) * 0.1).float()
+    pre = oi.scatter_qkv(oi.epilogue_rowcolscale(oi.i8_matmul2d_nt(a.numpy(), b.numpy()),
+                                                 rs.numpy(), cs.numpy(), bits16(bb)), H, 128)
+    ref = oqk.qkv_rms_rope(*pre, bits16(freqs), qw.numpy(), kw.numpy(), 1e-6)
+    return (a, b, rs, cs, bb, freqs, qw, kw), ref
+
+
+@pytest.mark.parametrize("route", ["two-pass", "fused", "fused-0", "fused-1", "fused-2"])
+@pytest.mark.parametrize("M,K,H,R", [(300, 1024, 4, 48), (1024, 3072, 24, 48), (777, 512, 3, 64),
+                                     (130, 256, 1, 8), (2100, 640, 7, 16), (130, 256, 1, 1),
+                                     (513, 128, 5, 33)])
+def test_i8_fused_cs_qkv_rms_rope_exact(dev, monkeypatch, route, M, K, H, R):
+    """H3 QKV + Q/K RMSNorm + partial RoPE: bit-exact to the oracle on both
+    routes -- the QKV scatter then the in-place norm/RoPE pass (default),
+    and the fused epilogue (R a multiple of 8; else it takes the two-pass
+    route too) with its default plan (256x256 8-wave tiles + 128x128 2-wave
+    tail) and each head tile forced. Odd head counts leave half of the last
+    256-column tile past N."""
+    if route != "two-pass":
+        monkeypatch.setenv("C4Q_QKV_NORM_FUSE", "1")
+    if route.startswith("fused-"):
+        monkeypatch.setenv("C4Q_HEAD_TILE", route[-1])
+    ins, ref = _qkv_rope_case(M, K, H, R, 7 + M + H + R)
+    a, b, rs, cs, bb, freqs, qw, kw = (t.to(dev) for t in ins)
+    outs = ops.i8_matmul2d_nt_fused_cs_qkv_rms_rope(a, b, rs, cs, bb, freqs, qw, kw, H, 128, 1e-6)
+    for name, o, r in zip("qkv", outs, ref):
+        assert o.shape == (1, H, M, 128)
+        assert_bits_equal(bits16(o), r, f"qkv-rms-rope {name} {M}x{K} H{H} R{R} {route}")
+
+
+@pytest.mark.parametrize("M,K,H,R", [(100, 200, 2, 48), (333, 1000, 3, 64)])
+def test_i8_fused_cs_qkv_rms_rope_generic_path(dev, M, K, H, R):
+    """K not a multiple of 16: the generic product + scatter, then the
+    in-place norm/RoPE pass -- the same bytes."""
+    ins, ref = _qkv_rope_case(M, K, H, R, 3 + M + R)
+    a, b, rs, cs, bb, freqs, qw, kw = (t.to(dev) for t in ins)
+    outs = ops.i8_matmul2d_nt_fused_cs_qkv_rms_rope(a, b, rs, cs, None if H == 3 else bb, freqs,
+                                                    qw, kw, H, 128, 1e-6)
+    if H == 3:
+        a0, b0, rs0, cs0 = ins[:4]
+        pre = oi.scatter_qkv(oi.epilogue_rowcolscale(oi.i8_matmul2d_nt(a0.numpy(), b0.numpy()),
+                                                     rs0.numpy(), cs0.numpy(), None), H, 128)
+        ref = oqk.qkv_rms_rope(*pre, bits16(ins[5]), ins[6].numpy(), ins[7].numpy(), 1e-6)
+    for name, o, r in zip("qkv", outs, ref):
+        assert_bits_equal(bits16(o), r, f"qkv-rms-rope generic {name} {M}x{K} H{H} R{R}")
+
+
+def test_i8_fused_cs_qkv_rms_rope_matches_scatter_then_norm(dev):
+    """V equals the plain QKV scatter's V; Q/K equal the oracle applied to
+    the scatter kernel's own Q/K (the epilogue adds norm/RoPE only)."""
+    M, K, H, R = 512, 1024, 6, 48
+    ins, _ = _qkv_rope_case(M, K, H, R, 99)
+    a, b, rs, cs, bb, freqs, qw, kw = (t.to(dev) for t in ins)
+    q, k, v = ops.i8_matmul2d_nt_fused_cs_qkv(a, b, rs, cs, bb, H, 128)
+    outs = ops.i8_matmul2d_nt_fused_cs_qkv_rms_rope(a, b, rs, cs, bb, freqs, qw, kw, H, 128, 1e-6)
+    assert_bits_equal(bits16(outs[2]), bits16(v), "V")
+    assert_bits_equal(bits16(outs[0]), oqk.qk_rms_rope(bits16(q), bits16(freqs), ins[6].numpy(),
+                                                       1e-6), "Q")
+    assert_bits_equal(bits16(outs[1]), oqk.qk_rms_rope(bits16(k), bits16(freqs), ins[7].numpy(),
+                                                       1e-6), "K")
+
+
+def test_i8_fused_cs_qkv_rms_rope_rejects_bad_shapes(dev):
+    a = torch.zeros(100, 64, dtype=torch.int8, device=dev)
+    b = torch.zeros(3 * 2 * 64, 64, dtype=torch.int8, device=dev)
+    rs = torch.ones(100, device=dev)
+    cs = torch.ones(384, device=dev)
+    fr = torch.zeros(100, 16, 2, 2, dtype=torch.bfloat16, device=dev)
+    w = torch.ones(128, device=dev)
+    with pytest.raises(C4QError, match="D=128"):
+        ops.i8_matmul2d_nt_fused_cs_qkv_rms_rope(a, b, rs, cs, None, fr, w, w, 2, 64, 1e-6)
+    b = torch.zeros(3 * 2 * 128, 64, dtype=torch.int8, device=dev)
+    cs = torch.ones(768, device=dev)
+    with pytest.raises(C4QError, match="freqs"):
+        ops.i8_matmul2d_nt_fused_cs_qkv_rms_rope(a, b, rs, cs, None, fr[:50], w, w, 2, 128, 1e-6)
 
 
 def test_c1_golden_digest_full_size(dev):

@@ -205,3 +205,42 @@ def test_o_proj_prequant_and_swiglu_forward_exact(dev):
     rq2, rs2 = oi.quant_rowwise(ocr.swiglu_rot(bits16(xf.reshape(70, 2 * F)), silu_dev), "bf16")
     ref2 = oi.epilogue_rowcolscale(oi.i8_matmul2d_nt(rq2, w2.numpy()), rs2.reshape(-1), ws.numpy())
     assert_bits_equal(bits16(y.reshape(70, N)), ref2, "swiglu fc2 patch")
+
+
+def test_qkv_prequant_routes_exact(dev):
+    """The H3 QKV routes of the INT8 linear patch on a stand-in
+    TensorWiseINT8Layout weight: layout-only and with Q/K RMSNorm + partial
+    RoPE, bit-exact against the oracle chain (rowwise quant, product,
+    per-channel epilogue, scatter, norm/RoPE)."""
+    import types
+    from oracle import qknorm as oqk
+
+    class QT:
+        _layout_cls = "TensorWiseINT8Layout"
+
+        def __init__(self, q, scale):
+            self._qdata = q
+            self._params = types.SimpleNamespace(scale=scale, convrot=False, transposed=False)
+
+    g = gen(33)
+    S, K, H, D, R = 200, 512, 3, 128, 48
+    x = (torch.randn(S, K, generator=g) * 2).to(torch.bfloat16)
+    w = _i8((3 * H * D, K), g)
+    ws = torch.rand(3 * H * D, generator=g) * 0.002
+    bias = (torch.randn(3 * H * D, generator=g) * 0.1).to(torch.bfloat16)
+    fr = torch.randn(1, S, 1, R, 2, 2, generator=g).to(torch.bfloat16)
+    qw = (1 + torch.randn(D, generator=g) * 0.1).float()
+    kw = (1 + torch.randn(D, generator=g) * 0.1).float()
+    layer = types.SimpleNamespace(weight=QT(w.to(dev), ws.to(dev)), bias=bias.to(dev),
+                                  weight_function=[], bias_function=[])
+    xq, xs = oi.quant_rowwise(bits16(x), "bf16")
+    pre = oi.scatter_qkv(oi.epilogue_rowcolscale(oi.i8_matmul2d_nt(xq, w.numpy()), xs.reshape(-1),
+                                                 ws.numpy(), bits16(bias)), H, D)
+    outs = int8_linear.int8_qkv_prequant(layer, x.to(dev), H, D)
+    for name, o, r in zip("qkv", outs, pre):
+        assert_bits_equal(bits16(o), r, f"qkv patch {name}")
+    ref = oqk.qkv_rms_rope(*pre, bits16(fr), qw.numpy(), kw.numpy(), 1e-6)
+    outs = int8_linear.int8_qkv_rms_rope_prequant(layer, x.to(dev), fr.to(dev), qw.to(dev),
+                                                  kw.to(dev), H, D, 1e-6)
+    for name, o, r in zip("qkv", outs, ref):
+        assert_bits_equal(bits16(o), r, f"qkv rms-rope patch {name}")

@@ -25,6 +25,7 @@ from oracle import convrot as ocr
 from oracle import fp8 as of
 from oracle import int8 as oi
 from oracle import pair as op
+from oracle import qknorm as oqk
 from oracle import torch_path as tp
 from oracle.numerics import (bf16_bits_to_f32, e4m3fn_decode, e4m3fn_encode, f16_bits_to_f32,
                              f32_to_bf16_bits, f32_to_f16_bits)
@@ -475,3 +476,118 @@ def test_scatter_qkv_is_the_torch_split_and_head_transpose():
     got = oi.scatter_qkv(tbits(y), h, d)
     for a, b in zip(got, want):
         assert np.array_equal(a, tbits(b))
+
+
+# ------------------------------------------------ Q/K RMSNorm + RoPE (H3) ---
+
+def _qk_inputs(seed, rows=37, heads=2, pairs=48):
+    g = torch.Generator().manual_seed(seed)
+    x = (torch.randn(1, heads, rows, 128, generator=g) * 2).to(torch.bfloat16)
+    freqs = torch.randn(rows, pairs, 2, 2, generator=g).to(torch.bfloat16)
+    w = (1 + torch.randn(128, generator=g) * 0.1).float()
+    return x, freqs, w
+
+
+def test_qknorm_sum_order_is_a_permutation_of_all_columns():
+    cols = sorted(c for j in range(8) for c in oqk.lane_columns(j))
+    assert cols == list(range(128))
+
+
+def test_qknorm_sum_of_squares_close_to_exact():
+    """The fixed fp32 order vs the float64 sum: 16 sequential adds plus 3
+    tree levels bound the relative error by 19 * 2^-24; a dropped or doubled
+    column moves it by far more."""
+    x, _, _ = _qk_inputs(51, rows=300)
+    xf = x.float().numpy()
+    exact = (xf.astype(np.float64) ** 2).sum(-1)
+    got = oqk.sum_squares(xf).astype(np.float64)
+    assert np.max(np.abs(got - exact) / exact) <= 19 * 2.0 ** -24
+    bad = xf.copy()
+    bad[..., 127] = 0
+    assert np.max(np.abs(oqk.sum_squares(bad) - exact) / exact) > 1e-4
+
+
+def test_qknorm_rms_against_torch_rms_norm():
+    """Against torch's F.rms_norm in fp32 (its own sum order), then bf16:
+    at most 1 bf16 ulp apart, and almost everywhere equal."""
+    x, _, w = _qk_inputs(52, rows=400)
+    got = oqk.rms_norm(tbits(x), w.numpy(), 1e-6)
+    want = F.rms_norm(x.float(), (128,), w, eps=1e-6).to(torch.bfloat16).float().numpy()
+    ulp = np.abs(tbits(torch.from_numpy(got).to(torch.bfloat16)).astype(np.int32)
+                 - tbits(torch.from_numpy(want).to(torch.bfloat16)).astype(np.int32))
+    assert ulp.max() <= 1
+    assert (ulp != 0).mean() < 0.01
+    # the weight on the wrong side of the rounding, or a missing eps, fails
+    assert not np.array_equal(oqk.rms_norm(tbits(x), np.ones(128, np.float32), 1e-6), got)
+
+
+def test_qknorm_eps_dominates_tiny_rows():
+    """A zero row stays zero; a tiny row is scaled by 1/sqrt(eps)."""
+    x = torch.zeros(1, 1, 2, 128, dtype=torch.bfloat16)
+    x[0, 0, 1, 0] = 2.0 ** -20
+    y = oqk.rms_norm(tbits(x), np.ones(128, np.float32), 1e-6)
+    assert np.all(y[0, 0, 0] == 0)
+    want = np.float32(2.0 ** -20) / np.sqrt(np.float32(2.0 ** -40 / 128 + 1e-6).astype(np.float32))
+    assert y[0, 0, 1, 0] == bf16_bits_to_f32(f32_to_bf16_bits(np.float32(want)))
+
+
+def test_rope_split_half_matches_torch_eager_form():
+    """comfy_kitchen's eager form on torch CPU bf16 tensors: out = y * diag;
+    out.addcmul_(partner, off) -- bit-exact."""
+    x, freqs, w = _qk_inputs(53, rows=64, pairs=48)
+    y = torch.from_numpy(oqk.rms_norm(tbits(x), w.numpy(), 1e-6)).to(torch.bfloat16)
+    R = 48
+    f = freqs                                   # [M, R, 2, 2]
+    y0, y1 = y[..., :R], y[..., R:2 * R]
+    o0 = y0 * f[:, :, 0, 0]
+    o0.addcmul_(y1, f[:, :, 0, 1])
+    o1 = y1 * f[:, :, 1, 1]
+    o1.addcmul_(y0, f[:, :, 1, 0])
+    want = torch.cat([o0, o1, y[..., 2 * R:]], dim=-1)
+    got = oqk.rope_split_half(y.float().numpy(), tbits(freqs), 64)
+    assert np.array_equal(got, tbits(want))
+
+
+def test_rope_closed_forms_pin_partner_and_row():
+    """Swap matrices [[0,1],[1,0]] exchange the halves exactly; a quarter
+    turn [[0,-1],[1,0]] gives (-y1, y0); identity keeps y; columns past 2R
+    are untouched."""
+    g = torch.Generator().manual_seed(54)
+    M, R = 5, 20
+    y = torch.randn(1, 3, M, 128, generator=g).to(torch.bfloat16).float()
+    yn = y.numpy()
+
+    def run(mat):
+        f = torch.tensor(mat, dtype=torch.bfloat16).expand(M, R, 2, 2).contiguous()
+        return bf16_bits_to_f32(oqk.rope_split_half(yn, tbits(f), M))
+
+    sw = run([[0.0, 1.0], [1.0, 0.0]])
+    assert np.array_equal(sw[..., :R], yn[..., R:2 * R]) and np.array_equal(sw[..., R:2 * R], yn[..., :R])
+    qt = run([[0.0, -1.0], [1.0, 0.0]])
+    assert np.array_equal(qt[..., :R], -yn[..., R:2 * R]) and np.array_equal(qt[..., R:2 * R], yn[..., :R])
+    ident = run([[1.0, 0.0], [0.0, 1.0]])
+    assert np.array_equal(ident, yn)
+    assert np.array_equal(sw[..., 2 * R:], yn[..., 2 * R:])
+
+
+def test_rope_rotation_preserves_pair_norm():
+    """cos/sin rotation matrices: |(out_i, out_{i+R})| = |(y_i, y_{i+R})| up
+    to bf16 rounding of the inputs and outputs."""
+    g = torch.Generator().manual_seed(55)
+    M, R = 16, 48
+    y = torch.randn(1, 2, M, 128, generator=g).to(torch.bfloat16).float()
+    th = torch.rand(M, R, generator=g) * 6.28
+    f = torch.stack([torch.stack([th.cos(), -th.sin()], -1), torch.stack([th.sin(), th.cos()], -1)], -2)
+    out = bf16_bits_to_f32(oqk.rope_split_half(y.numpy(), tbits(f.to(torch.bfloat16)), M))
+    n_in = np.hypot(y.numpy()[..., :R], y.numpy()[..., R:2 * R])
+    n_out = np.hypot(out[..., :R], out[..., R:2 * R])
+    assert np.allclose(n_out, n_in, rtol=3e-2, atol=1e-2)
+
+
+def test_qkv_rms_rope_keeps_v_and_uses_each_weight():
+    x, freqs, w = _qk_inputs(56, rows=9)
+    q, k, v = oqk.qkv_rms_rope(tbits(x), tbits(x), tbits(x), tbits(freqs), w.numpy(),
+                               np.ones(128, np.float32), 1e-6)
+    assert np.array_equal(v, tbits(x))
+    assert np.array_equal(q, oqk.qk_rms_rope(tbits(x), tbits(freqs), w.numpy(), 1e-6))
+    assert not np.array_equal(q, k)

@@ -16,6 +16,7 @@ import torch
 
 import cdna4q.ops as ops
 from cdna4q import _lib
+from cdna4q._lib import C4QError
 from cdna4q.patches import (_common, int8_linear, int_mm, krea2_ffn_pair, linear_fp8_w8a16,
                             moss_ffn, scaled_mm_fp8)
 import cdna4q.patches as patches
@@ -207,6 +208,46 @@ def test_o_proj_prequant_gate(cpu_gate, monkeypatch):
     assert f(_layer(FakeQT(q, torch.rand(16), convrot=True, transposed=True)), x) is None
     monkeypatch.setenv("C4Q_INT8_OPROJ_FUSE", "0")
     assert f(_layer(FakeQT(q, torch.rand(16), convrot=True)), x) is None
+
+
+def test_qkv_prequant_gate(cpu_gate, monkeypatch):
+    seen = []
+    monkeypatch.setattr(int8_linear, "_quant_cached",
+                        lambda x, *a: (torch.zeros(x.shape, dtype=torch.int8), torch.ones(x.shape[0], 1)))
+    monkeypatch.setattr(ops, "i8_matmul2d_nt_fused_cs_qkv",
+                        lambda *a: seen.append(("scatter", a[-2:])) or "qkv")
+    monkeypatch.setattr(ops, "i8_matmul2d_nt_fused_cs_qkv_rms_rope",
+                        lambda *a: seen.append(("rope", a[-3:])) or "qkv-rope")
+    H, D, K = 2, 128, 64
+    x = torch.zeros(70, K, dtype=torch.bfloat16)
+    q = _i8((3 * H * D, K), 1)
+    layer = _layer(FakeQT(q, torch.rand(3 * H * D)))
+    fr = torch.zeros(70, 48, 2, 2, dtype=torch.bfloat16)
+    w = torch.ones(D)
+    assert int8_linear.int8_qkv_prequant(layer, x, H, D) == "qkv"
+    assert int8_linear.int8_qkv_rms_rope_prequant(layer, x, fr, w, w, H, D, 1e-6) == "qkv-rope"
+    assert seen == [("scatter", (H, D)), ("rope", (H, D, 1e-6))]
+    f = int8_linear.int8_qkv_prequant
+    assert f(layer, x.float(), H, D) is None                                   # not bf16
+    assert f(layer, x.unsqueeze(0), H, D) is None                              # not 2-D
+    assert f(layer, x, 3, D) is None                                           # width != 3HD
+    assert f(_layer(FakeQT(q, torch.rand(3 * H * D), convrot=True)), x, H, D) is None
+    assert f(_layer(FakeQT(q, torch.rand(7))), x, H, D) is None                 # scale layout
+    lora = _layer(FakeQT(q, torch.rand(3 * H * D)))
+    lora._asfp8_runtime_lora = object()
+    assert f(lora, x, H, D) is None
+    monkeypatch.setenv("C4Q_INT8_QKV_NORM_ROPE", "0")
+    assert int8_linear.int8_qkv_rms_rope_prequant(layer, x, fr, w, w, H, D, 1e-6) is None
+    assert f(layer, x, H, D) == "qkv"
+    monkeypatch.setenv("C4Q_INT8_QKV_SCATTER", "0")
+    assert f(layer, x, H, D) is None
+    # a rejected call (the kernel wrapper raises) falls back
+    monkeypatch.delenv("C4Q_INT8_QKV_SCATTER")
+
+    def bad(*a):
+        raise C4QError("freqs shape mismatch")
+    monkeypatch.setattr(ops, "i8_matmul2d_nt_fused_cs_qkv", bad)
+    assert f(layer, x, H, D) is None
 
 
 def test_swiglu_forward_routes(cpu_gate, monkeypatch):

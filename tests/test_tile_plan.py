@@ -115,3 +115,59 @@ def test_tail_of_128x128_pieces(probe):
     _, info = plan(probe, 4608, 4608, 1024, 256)
     assert info[0] == 2 and (info[1], info[2]) == (TILE_256, 256)
     assert (info[3], info[4]) == (TILE_128_K128, 68 * 4) and (info[6], info[7]) == (2, 2)
+
+
+# ------------------------------------------------- head-spanning tile set ---
+# HeadTiles (the QKV + RMSNorm/RoPE epilogue): every wave spans one whole
+# 128-column head, so every tile's columns start at a multiple of 128. The
+# planner picks among ids 0 and 1 (id 2, the 4-wave 256x256 tile, is only
+# forced for sweeps).
+HEAD_256 = 0       # 256x256, 8 waves of 64x128
+HEAD_128 = 1       # 128x128, 2 waves of 64x128
+
+
+@pytest.fixture(scope="module")
+def head_probe():
+    if not LIB.exists():
+        subprocess.run(["make", "-C", str(NATIVE)], check=True)
+    lib = ctypes.CDLL(str(LIB))
+    f = lib.c4q_probe_head_tile_plan
+    f.argtypes = [ctypes.c_int64] * 3 + [ctypes.c_int, ctypes.c_void_p, ctypes.c_int64,
+                                         ctypes.c_void_p]
+    f.restype = ctypes.c_int
+    return f
+
+
+# (M, N = 3 * heads * 128, K): H3 (56 heads, hidden 5376) at its three token
+# counts, 24 heads (FLUX width), an odd head count, small M
+HEAD_SHAPES = [(5378, 21504, 5376), (8192, 21504, 5376), (17000, 21504, 5376),
+               (4096, 9216, 3072), (4608, 3 * 7 * 128, 1024), (65, 384, 128), (300, 3 * 5 * 128, 64)]
+
+
+@pytest.mark.parametrize("cus", [256, 304, 80])
+@pytest.mark.parametrize("M,N,K", HEAD_SHAPES)
+def test_head_plan_every_cell_once(head_probe, M, N, K, cus):
+    cover, info = plan(head_probe, M, N, K, cus)
+    assert info[0] in (1, 2)
+    assert {info[1], info[3] if info[0] == 2 else HEAD_256} <= {HEAD_256, HEAD_128}
+    assert cover.min() == 1 and cover.max() == 1, (M, N, K, cus, info.tolist())
+
+
+def test_head_plan_random_shapes(head_probe):
+    rng = np.random.default_rng(2)
+    for _ in range(200):
+        M = int(rng.integers(1, 20000))
+        N = 384 * int(rng.integers(1, 64))
+        K = int(rng.choice([64, 1024, 5376]))
+        cus = int(rng.choice([256, 304, 120]))
+        cover, info = plan(head_probe, M, N, K, cus)
+        assert cover.min() == 1 and cover.max() == 1, (M, N, K, cus, info.tolist())
+
+
+def test_head_plan_h3_8192(head_probe):
+    """H3 at 8192 tokens: 32 x 84 = 2688 tiles of 256x256, ten whole rounds
+    on 256 CUs (2560) and 128 leftover tiles as 512 pieces of 128x128, one
+    round of two workgroups per CU."""
+    _, info = plan(head_probe, 8192, 21504, 5376, 256)
+    assert info[0] == 2 and (info[1], info[2]) == (HEAD_256, 2560)
+    assert (info[3], info[4]) == (HEAD_128, 512) and (info[6], info[7]) == (2, 2)
