@@ -241,6 +241,33 @@ extern "C" int c4q_i8_gemm_nt_fused_cs_qkv_rms_rope(
   return check_launch(what);
 }
 
+extern "C" int c4q_i8_mlp_bridge_prequant(const int8_t* a, int64_t lda, const int8_t* w1,
+                                          int64_t ldw, const float* row_scale,
+                                          const float* col_scale, const uint16_t* bias,
+                                          const uint16_t* silu_table, int64_t M, int64_t K,
+                                          int64_t W, int64_t tile_rows, uint16_t* wide,
+                                          uint16_t* rot, int8_t* q, float* scales, void* stream) {
+  const char* what = "c4q_i8_mlp_bridge_prequant";
+  C4Q_REQUIRE(M >= 0 && K >= 0 && W > 0 && W % 512 == 0, C4Q_ERR_SHAPE,
+              "%s: need W = 2F > 0 with F a multiple of 256 (W=%lld)", what, (long long)W);
+  C4Q_REQUIRE(tile_rows > 0, C4Q_ERR_SHAPE, "%s: tile_rows must be positive", what);
+  if (M == 0) return C4Q_OK;
+  C4Q_REQUIRE(wide && rot && q && scales && silu_table, C4Q_ERR_ARG, "%s: null buffer", what);
+  const int64_t F = W / 2;
+  // per chunk of rows: FC1 with the per-channel epilogue into `wide`, the
+  // SwiGLU + ConvRot pass into `rot`, rowwise quant into the chunk's q rows
+  for (int64_t r0 = 0; r0 < M; r0 += tile_rows) {
+    const int64_t rows = M - r0 < tile_rows ? M - r0 : tile_rows;
+    int st = c4q_i8_gemm_nt_fused_cs(a + r0 * lda, lda, w1, ldw, wide, W, row_scale + r0, col_scale,
+                                     bias, rows, W, K, stream);
+    if (st == C4Q_OK) st = c4q_i8_swiglu_rot(wide, rows, F, silu_table, rot, stream);
+    if (st == C4Q_OK)
+      st = c4q_i8_quant_rowwise(rot, C4Q_BF16, F, q + r0 * F, F, scales + r0, rows, F, stream);
+    if (st != C4Q_OK) return st;
+  }
+  return C4Q_OK;
+}
+
 extern "C" int c4q_i8_ffn_pair(const int8_t* a, int64_t lda, const int8_t* w_gate,
                                const int8_t* w_up, int64_t ldw, uint16_t* d, int64_t ldd,
                                const float* row_scale, const float* gate_scale,

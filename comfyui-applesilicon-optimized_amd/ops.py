@@ -255,6 +255,49 @@ def i8_matmul2d_nt_fused_cs_qkv_rms_rope(a_i8, b_i8, row_scale, col_scale, bias,
     return outs
 
 
+# Chunk of FC1 rows of the MLP bridge when the caller asks for "auto": the
+# bf16 FC1 chunk and its rotated half stay in the Infinity Cache between the
+# three passes (H3 W = 28672: 2048 rows are 117 + 59 MB).
+MLP_BRIDGE_AUTO_ROWS = 2048
+
+
+def i8_mlp_bridge_prequant(a_i8, fc1_weight, row_scale, fc1_col_scale, fc1_bias=None,
+                           long_schedule=True, tile_rows=-1):
+    """H3 FC1/SwiGLU/FC2 bridge, front half: (q [M, F] int8, scales [M, 1]
+    fp32), FC2's ConvRot-rotated rowwise-quantized activation, from the int8
+    FC1 input without storing FC1's [M, 2F] output whole
+    (_patches/int8_ext/int8_gemm.mm:2377-2537). tile_rows: -1 auto, 0 all
+    rows at once, else at least 128 (rounded down to a multiple of 128).
+    long_schedule selects a reference tile order that changes no byte."""
+    del long_schedule
+    dev, lda, ldw = _i8_operands(a_i8, fc1_weight)
+    _req(a_i8.is_contiguous() and fc1_weight.is_contiguous(),
+         "activation and FC1 weight must be contiguous 2D tensors")
+    M, K = a_i8.shape
+    W = fc1_weight.size(0)
+    _req(M > 64 and W > 0 and W % 512 == 0, "bridge requires M > 64 and F divisible by 256")
+    _req(tile_rows == -1 or tile_rows == 0 or tile_rows >= 128,
+         "tile_rows must be -1 (auto), zero, or at least 128")
+    _dev(row_scale, fc1_col_scale, fc1_bias)
+    _vec(row_scale, M, torch.float32, "row_scale")
+    _vec(fc1_col_scale, W, torch.float32, "fc1_col_scale")
+    bias = _bias_bf16(fc1_bias, W)
+    rows = M if tile_rows == 0 else min(M, MLP_BRIDGE_AUTO_ROWS if tile_rows < 0 else tile_rows)
+    rows = rows // 128 * 128 if rows >= 128 else rows
+    F = W // 2
+    wide = torch.empty((rows, W), dtype=torch.bfloat16, device=dev)
+    rot = torch.empty((rows, F), dtype=torch.bfloat16, device=dev)
+    q = torch.empty((M, F), dtype=torch.int8, device=dev)
+    scales = torch.empty((M, 1), dtype=torch.float32, device=dev)
+    silu = act_table("silu", dev)
+    with _on(dev):
+        _lib.call("c4q_i8_mlp_bridge_prequant", a_i8.data_ptr(), lda, fc1_weight.data_ptr(), ldw,
+                  row_scale.data_ptr(), fc1_col_scale.data_ptr(),
+                  bias.data_ptr() if bias is not None else None, silu.data_ptr(), M, K, W, rows,
+                  wide.data_ptr(), rot.data_ptr(), q.data_ptr(), scales.data_ptr(), _stream(dev))
+    return q, scales
+
+
 def i8_merge_rot_quant(x, rotate=True):
     """x [B,H,S,D] bf16 (attention layout) -> (q [B*S, H*D] int8,
     scales [B*S, 1] fp32): head merge, ConvRot rotation of every 256-element

@@ -10,18 +10,20 @@ reference patch:
     krea2_ffn_pair    Krea2 SwiGLU gate/up pair      (_patches/krea2_ffn_pair.py)
     moss_ffn          MOSS FC1 + SiTU pair           (_patches/moss_ffn_mps.py)
     moss_bf16_ffn_pair  MOSS bf16 FC1 + SiTU pair    (_patches/moss_bf16_ffn_pair.py)
+    quant_meta_fix    comfy_quant metadata repair    (_patches/quant_meta_fix.py)
 
 ``install_all()`` installs every patch whose host (a ROCm device, ComfyUI for
 the model seams) is present and returns the names installed. Each module also
 honours its own ``C4Q_<NAME>=0`` switch.
 """
 from . import (int8_linear, int_mm, krea2_ffn_pair, linear_fp8_w8a16, moss_bf16_ffn_pair, moss_ffn,
-               scaled_mm_fp8)
+               quant_meta_fix, scaled_mm_fp8)
 from . import _common
 
 _ALL = (("int_mm", int_mm), ("scaled_mm_fp8", scaled_mm_fp8), ("int8_linear", int8_linear),
         ("linear_fp8_w8a16", linear_fp8_w8a16), ("krea2_ffn_pair", krea2_ffn_pair),
-        ("moss_ffn", moss_ffn), ("moss_bf16_ffn_pair", moss_bf16_ffn_pair))
+        ("moss_ffn", moss_ffn), ("moss_bf16_ffn_pair", moss_bf16_ffn_pair),
+        ("quant_meta_fix", quant_meta_fix))
 
 
 def install_all():

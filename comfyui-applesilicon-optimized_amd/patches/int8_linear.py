@@ -33,10 +33,19 @@ Mirrors ``_patches/int8_linear_kernel_mps.py`` (and the int8-fast seam of
   rowwise quant and the INT8 GEMM; otherwise the bf16 SwiGLU and the
   ordinary W8A8 path.
 
-Not supported here (those calls keep the original function): the generic
-ConvRot rotation of ``int8_linear(..., convrot=True)`` (comfy_kitchen's eager
-Hadamard matmul; its rounding is not pinned), non-int8 weights, tensors off
-the ROCm device.
+* ``int8_qkv_prequant`` / ``int8_qkv_rms_rope_prequant`` are the H3 QKV
+  projection straight into the attention layout, optionally with the Q/K
+  RMSNorm + partial RoPE epilogue (``:266-432``);
+* ``int8_mlp_bridge`` is the H3 FC1 -> SwiGLU -> ConvRot -> FC2 chain with
+  FC1's output chunked through the bridge (``:538-673``).
+
+ConvRot activations (``int8_linear(..., convrot=True)`` and ConvRot layer
+weights) are rotated by the fused rotate + quant pass when they are bf16
+with K % 256 == 0 and K <= 15360, group size 256; the reference rotates
+with comfy_kitchen's eager Hadamard matmul (same values up to fp32
+summation order; comfy_kitchen is not available, so that equivalence is
+unpinned). Not supported here (those calls keep the original function):
+other ConvRot inputs, non-int8 weights, tensors off the ROCm device.
 """
 import os
 import weakref
@@ -55,17 +64,40 @@ _act_cache = None      # (x_weakref, convrot, groupsize, x_8, x_scale)
 _RESCALE_CHUNK_BYTES = 256 * 1024 * 1024
 
 
+def _convrot_ok(x, convrot_groupsize):
+    """ConvRot activations this build rotates: bf16, group size 256, rows of
+    K % 256 == 0 elements that fit the fused pass (K <= 15360)."""
+    k = x.shape[-1]
+    return (convrot_groupsize == 256 and x.dtype == torch.bfloat16 and k % 256 == 0
+            and k * 2 <= 30 * 1024)
+
+
 def _quant_cached(x, convrot=False, convrot_groupsize=256):
-    """Rowwise-quantize x (reference ``:97-140``), reusing the previous result
-    when the same live tensor object is quantized again with the same
-    settings. Disable with ``C4Q_INT8_ACT_CACHE=0``."""
+    """Rotate (ConvRot) and rowwise-quantize x (reference ``:97-140``),
+    reusing the previous result when the same live tensor object is
+    quantized again with the same settings. Disable the reuse with
+    ``C4Q_INT8_ACT_CACHE=0``.
+
+    The rotation is the 256-wide normalized Hadamard of every group, done
+    by the fused rotate + quant pass with x viewed as [M, K/256, 1, 256]
+    heads (its head merge is then the identity). The reference rotates with
+    comfy_kitchen's Hadamard matmul (``_rotate_activation``): the same
+    values up to the fp32 summation order before the bf16 rounding, the
+    order the reference's own fused passes use."""
     global _act_cache
-    if convrot:
-        raise C4QError(f"{TAG} ConvRot activation rotation is not supported by this build")
+    if convrot and not _convrot_ok(x, convrot_groupsize):
+        raise C4QError(f"{TAG} ConvRot rotation needs bf16 rows of K % 256 == 0, K <= 15360 "
+                       f"and group size 256 (K={x.shape[-1]}, {x.dtype}, "
+                       f"group {convrot_groupsize})")
     c = _act_cache
     if c is not None and c[0]() is x and c[1] == convrot and c[2] == convrot_groupsize:
         return c[3], c[4]
-    x_8, x_scale = ops.i8_quant_rowwise(x.reshape(-1, x.shape[-1]))
+    x2 = x.reshape(-1, x.shape[-1])
+    if convrot:
+        k = x2.shape[1]
+        x_8, x_scale = ops.i8_merge_rot_quant(x2.contiguous().view(x2.shape[0], k // 256, 1, 256))
+    else:
+        x_8, x_scale = ops.i8_quant_rowwise(x2)
     if os.environ.get("C4Q_INT8_ACT_CACHE", "1") != "0":
         try:
             _act_cache = (weakref.ref(x), convrot, convrot_groupsize, x_8, x_scale)
@@ -111,8 +143,8 @@ def _int8_linear_kernel(x, weight, weight_scale, bias=None, out_dtype=torch.bflo
     """Kernel-backed drop-in for comfy_kitchen's eager ``int8_linear``
     (reference ``:218-263``). Calls it cannot serve go to the original
     function when one is installed, else raise."""
-    if (convrot or weight.dtype != torch.int8 or not _common.on_device(x, weight)
-            or x.dtype not in (torch.bfloat16, torch.float16)):
+    if ((convrot and not _convrot_ok(x, convrot_groupsize)) or weight.dtype != torch.int8
+            or not _common.on_device(x, weight) or x.dtype not in (torch.bfloat16, torch.float16)):
         if _orig_int8_linear is not None:
             return _orig_int8_linear(x, weight, weight_scale, bias, out_dtype, convrot,
                                      convrot_groupsize)
@@ -129,8 +161,9 @@ def _try_int8_kernel_forward(self, input):
     """Layer output via the kernel W8A8 path, or None to use comfy's forward
     (reference ``:779-830``). Eligible iff the input is a plain tensor on the
     ROCm device, the weight a TensorWiseINT8Layout QuantizedTensor without
-    ConvRot or transposition, and the layer has no full-precision flag,
-    force-cast or LoRA weight/bias functions."""
+    transposition (with ConvRot: an input the rotation pass takes), and the
+    layer has no full-precision flag, force-cast or LoRA weight/bias
+    functions."""
     if not _common.on_device(input) or _common.is_quantized_int8(input):
         return None
     w = getattr(self, "weight", None)
@@ -141,11 +174,15 @@ def _try_int8_kernel_forward(self, input):
     if len(getattr(self, "weight_function", [])) or len(getattr(self, "bias_function", [])):
         return None
     params = w._params
-    if getattr(params, "transposed", False) or getattr(params, "convrot", False):
+    if getattr(params, "transposed", False):
         return None
     if input.dtype not in (torch.bfloat16, torch.float16):
         return None
-    return _int8_linear_kernel(input, w._qdata, params.scale, self.bias, input.dtype)
+    convrot = bool(getattr(params, "convrot", False))
+    gs = getattr(params, "convrot_groupsize", 256)
+    if convrot and not _convrot_ok(input, gs):
+        return None
+    return _int8_linear_kernel(input, w._qdata, params.scale, self.bias, input.dtype, convrot, gs)
 
 
 def _plain_int8_layer(layer):
@@ -253,6 +290,54 @@ def int8_o_proj_prequant(layer, out_bhsd):
     x_8, x_scale = ops.i8_merge_rot_quant(out_bhsd.contiguous())
     return _int8_linear_prequant(x_8, x_scale, qdata.contiguous(), params.scale, layer.bias,
                                  torch.bfloat16, (B, S, H * D))
+
+
+def int8_mlp_bridge(fc1, fc2, x):
+    """H3 INT8 FC1 -> SwiGLU -> ConvRot -> FC2 without storing FC1's [M, 2F]
+    output whole (reference ``:538-673``): x [M, K] bf16 -> [M, N2] bf16, or
+    None when a check fails. FC1 runs chunk by chunk through the bridge
+    (``ops.i8_mlp_bridge_prequant``), FC2 on its quantized activation.
+    Requires per-channel scales on both layers and a ConvRot FC2 (group
+    256); runtime LoRA adapters are not served. Switches:
+    ``C4Q_INT8_MLP_BRIDGE=0`` (or ``ASFP8_INT8_MLP_BRIDGE``,
+    ``ASFP8_INT8_SWIGLU``, ``ASFP8_INT8_SWIGLU_ROT`` = 0)."""
+    if (os.environ.get("C4Q_INT8_MLP_BRIDGE", os.environ.get("ASFP8_INT8_MLP_BRIDGE", "1")) != "1"
+            or os.environ.get("ASFP8_INT8_SWIGLU", "1") != "1"
+            or os.environ.get("ASFP8_INT8_SWIGLU_ROT", "1") != "1"):
+        return None
+    if any(getattr(layer, "_asfp8_runtime_lora", None) is not None for layer in (fc1, fc2)):
+        return None
+    if (not isinstance(x, torch.Tensor) or x.dim() != 2 or not _common.on_device(x)
+            or x.dtype != torch.bfloat16 or not x.is_contiguous()):
+        return None
+    w1, w2 = _plain_int8_layer(fc1), _plain_int8_layer(fc2)
+    if w1 is None or w2 is None:
+        return None
+    p1, p2 = w1._params, w2._params
+    if not getattr(p2, "convrot", False) or getattr(p2, "convrot_groupsize", 256) != 256:
+        return None
+    q1, q2 = w1._qdata, w2._qdata
+    if (q1.dim() != 2 or q2.dim() != 2 or q1.shape[0] % 512 or q1.shape[1] != x.shape[1]
+            or q2.shape[1] * 2 != q1.shape[0]):
+        return None
+    s1, s2 = p1.scale.reshape(-1), p2.scale.reshape(-1)
+    if s1.numel() != q1.shape[0] or s2.numel() != q2.shape[0]:
+        return None
+    convrot1 = bool(getattr(p1, "convrot", False))
+    gs1 = getattr(p1, "convrot_groupsize", 256)
+    if convrot1 and not _convrot_ok(x, gs1):
+        return None
+    try:
+        x_8, x_scale = _quant_cached(x, convrot1, gs1)
+        bias1 = fc1.bias.to(torch.bfloat16) if fc1.bias is not None else None
+        fc2_8, fc2_scale = ops.i8_mlp_bridge_prequant(
+            x_8.contiguous(), q1.contiguous(), x_scale.reshape(-1).float().contiguous(),
+            s1.float().contiguous(), bias1)
+        return _int8_linear_prequant(fc2_8, fc2_scale, q2, s2, fc2.bias, x.dtype, x.shape,
+                                     split_tail=True)
+    except C4QError as e:
+        print(f"{TAG} MLP bridge fell back ({e})")
+        return None
 
 
 def _try_int8_swiglu_forward(linear, x):

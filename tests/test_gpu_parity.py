@@ -411,6 +411,30 @@ def test_i8_fused_cs_qkv_rms_rope_rejects_bad_shapes(dev):
         ops.i8_matmul2d_nt_fused_cs_qkv_rms_rope(a, b, rs, cs, None, fr[:50], w, w, 2, 128, 1e-6)
 
 
+@pytest.mark.parametrize("M,K,F,tile_rows", [(300, 512, 256, -1), (1000, 256, 512, 128),
+                                              (1000, 256, 512, 200), (700, 128, 256, 0),
+                                              (2500, 384, 256, -1)])
+def test_i8_mlp_bridge_prequant_exact(dev, M, K, F, tile_rows):
+    """FC1 -> SwiGLU -> ConvRot -> rowwise quant, chunk by chunk: the bytes of
+    the unfused oracle chain for every chunking (auto, 128-row chunks, 200
+    rounded down to 128, all rows at once; ragged last chunks)."""
+    g = gen(5 + M + F)
+    W = 2 * F
+    a, w1 = _randint8((M, K), g), _randint8((W, K), g)
+    rs = torch.rand(M, generator=g) * 0.01
+    cs = torch.rand(W, generator=g) * 0.02
+    bb = torch.randn(W, generator=g).to(torch.bfloat16)
+    q, sc = ops.i8_mlp_bridge_prequant(a.to(dev), w1.to(dev), rs.to(dev), cs.to(dev), bb.to(dev),
+                                       tile_rows=tile_rows)
+    fc1 = oi.epilogue_rowcolscale(oi.i8_matmul2d_nt(a.numpy(), w1.numpy()), rs.numpy(), cs.numpy(),
+                                  bits16(bb))
+    silu = ops.act_table("silu", dev).cpu().numpy().view(np.uint16)
+    rq, rsc = oi.quant_rowwise(ocr.swiglu_rot(fc1, silu), "bf16")
+    assert q.shape == (M, F) and sc.shape == (M, 1)
+    assert np.array_equal(q.cpu().numpy(), rq), f"bridge q {M}x{K} F{F} tile {tile_rows}"
+    assert np.array_equal(sc.cpu().numpy().reshape(-1), np.asarray(rsc).reshape(-1)), "bridge scales"
+
+
 def test_c1_golden_digest_full_size(dev):
     """BASELINE C1 at full size (seed 1): the kernel's INT32 product and
     per-channel bf16 epilogue hash to the digests written from torch._int_mm

@@ -244,3 +244,40 @@ def test_qkv_prequant_routes_exact(dev):
                                                   kw.to(dev), H, D, 1e-6)
     for name, o, r in zip("qkv", outs, ref):
         assert_bits_equal(bits16(o), r, f"qkv rms-rope patch {name}")
+
+
+def test_mlp_bridge_route_exact(dev):
+    """int8_mlp_bridge(fc1, fc2, x) on stand-in TensorWiseINT8Layout weights
+    (FC2 ConvRot): the FC2 output of the oracle chain, bit-exact."""
+    import types
+    from oracle import convrot as ocr
+
+    class QT:
+        _layout_cls = "TensorWiseINT8Layout"
+
+        def __init__(self, q, scale, convrot):
+            self._qdata = q
+            self._params = types.SimpleNamespace(scale=scale, convrot=convrot, transposed=False,
+                                                 convrot_groupsize=256)
+
+    g = gen(35)
+    M, K, F, N2 = 400, 512, 512, 384
+    x = (torch.randn(M, K, generator=g) * 2).to(torch.bfloat16)
+    w1, w2 = _i8((2 * F, K), g), _i8((N2, F), g)
+    s1, s2 = torch.rand(2 * F, generator=g) * 0.002, torch.rand(N2, generator=g) * 0.002
+    b1 = (0.1 * torch.randn(2 * F, generator=g)).to(torch.bfloat16)
+    b2 = (0.1 * torch.randn(N2, generator=g)).to(torch.bfloat16)
+    fc1 = types.SimpleNamespace(weight=QT(w1.to(dev), s1.to(dev), False), bias=b1.to(dev),
+                                weight_function=[], bias_function=[])
+    fc2 = types.SimpleNamespace(weight=QT(w2.to(dev), s2.to(dev), True), bias=b2.to(dev),
+                                weight_function=[], bias_function=[])
+    out = int8_linear.int8_mlp_bridge(fc1, fc2, x.to(dev))
+    assert out.shape == (M, N2)
+    xq, xs = oi.quant_rowwise(bits16(x), "bf16")
+    h = oi.epilogue_rowcolscale(oi.i8_matmul2d_nt(xq, w1.numpy()), xs.reshape(-1), s1.numpy(),
+                                bits16(b1))
+    silu = ops.act_table("silu", dev).cpu().numpy().view(np.uint16)
+    rq, rs = oi.quant_rowwise(ocr.swiglu_rot(h, silu), "bf16")
+    ref = oi.epilogue_rowcolscale(oi.i8_matmul2d_nt(rq, w2.numpy()), rs.reshape(-1), s2.numpy(),
+                                  bits16(b2))
+    assert_bits_equal(bits16(out), ref, "mlp bridge route")

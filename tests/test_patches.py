@@ -150,12 +150,38 @@ def test_int8_linear_unsupported_calls(cpu_gate, monkeypatch):
     monkeypatch.setattr(int8_linear, "_orig_int8_linear", None)
     with pytest.raises(_lib.C4QError):
         int8_linear.int8_linear(x, _i8((8, 16), 1), torch.tensor([1.0]), None, torch.bfloat16,
-                                True, 256)                           # convrot
+                                True, 256)                           # convrot, K % 256
     orig = Rec(lambda *a: "kitchen")
     monkeypatch.setattr(int8_linear, "_orig_int8_linear", orig)
     assert int8_linear.int8_linear(x, _i8((8, 16), 1), torch.tensor([1.0]), None,
                                    torch.bfloat16, True, 256) == "kitchen"
     assert int8_linear.int8_linear(x, torch.randn(8, 16), torch.tensor([1.0])) == "kitchen"
+
+
+def test_int8_linear_convrot_routes(cpu_gate, monkeypatch):
+    """ConvRot activations go through the fused rotate + quant pass, x viewed
+    as [M, K/256, 1, 256]; other group sizes, dtypes and widths keep the
+    original function."""
+    rec = _fake_int8_ops(monkeypatch)
+    seen = []
+
+    def mrq(xv):
+        seen.append(tuple(xv.shape))
+        return torch.zeros(xv.shape[0], xv.shape[1] * xv.shape[3], dtype=torch.int8), \
+            torch.ones(xv.shape[0], 1)
+    monkeypatch.setattr(ops, "i8_merge_rot_quant", mrq)
+    orig = Rec(lambda *a: "kitchen")
+    monkeypatch.setattr(int8_linear, "_orig_int8_linear", orig)
+    x = torch.randn(2, 3, 512).to(torch.bfloat16)
+    w = _i8((8, 512), 1)
+    out = int8_linear.int8_linear(x, w, torch.rand(8), None, torch.bfloat16, True, 256)
+    assert out.shape == (2, 3, 8) and seen == [(6, 2, 1, 256)] and "quant" not in rec
+    assert int8_linear.int8_linear(x, w, torch.rand(8), None, torch.bfloat16, True, 128) == "kitchen"
+    assert int8_linear.int8_linear(x.half(), w, torch.rand(8), None, torch.float16, True,
+                                   256) == "kitchen"
+    xw = torch.randn(2, 16384).to(torch.bfloat16)
+    assert int8_linear.int8_linear(xw, _i8((8, 16384), 1), torch.rand(8), None, torch.bfloat16,
+                                   True, 256) == "kitchen"           # K > 15360
 
 
 class FakeQT:
@@ -178,7 +204,11 @@ def test_try_int8_kernel_forward_eligibility(cpu_gate, monkeypatch):
     q = _i8((8, 16), 1)
     f = int8_linear._try_int8_kernel_forward
     assert f(_layer(FakeQT(q, torch.tensor([0.1]))), x) == "kernel"
-    assert f(_layer(FakeQT(q, torch.tensor([0.1]), convrot=True)), x) is None
+    assert f(_layer(FakeQT(q, torch.tensor([0.1]), convrot=True)), x) is None   # K % 256
+    q2 = _i8((8, 256), 1)
+    x2 = torch.randn(3, 256).to(torch.bfloat16)
+    assert f(_layer(FakeQT(q2, torch.tensor([0.1]), convrot=True)), x2) == "kernel"
+    assert fake.calls[-1][0][-2:] == (True, 256)
     assert f(_layer(FakeQT(q, torch.tensor([0.1]), transposed=True)), x) is None
     assert f(_layer(q), x) is None                                   # plain int8 weight
     assert f(_layer(FakeQT(q, torch.tensor([0.1])), _full_precision_mm=True), x) is None
@@ -187,7 +217,7 @@ def test_try_int8_kernel_forward_eligibility(cpu_gate, monkeypatch):
     lora.weight_function = [lambda w: w]
     assert f(lora, x) is None
     assert f(_layer(FakeQT(q, torch.tensor([0.1]))), x.float()) is None
-    assert len(fake.calls) == 1
+    assert len(fake.calls) == 2
 
 
 def test_o_proj_prequant_gate(cpu_gate, monkeypatch):
@@ -248,6 +278,33 @@ def test_qkv_prequant_gate(cpu_gate, monkeypatch):
         raise C4QError("freqs shape mismatch")
     monkeypatch.setattr(ops, "i8_matmul2d_nt_fused_cs_qkv", bad)
     assert f(layer, x, H, D) is None
+
+
+def test_mlp_bridge_gate(cpu_gate, monkeypatch):
+    seen = []
+    monkeypatch.setattr(int8_linear, "_quant_cached",
+                        lambda x, *a: (torch.zeros(x.shape, dtype=torch.int8), torch.ones(x.shape[0], 1)))
+    monkeypatch.setattr(ops, "i8_mlp_bridge_prequant",
+                        lambda x8, w1, rs, cs, b: seen.append(tuple(w1.shape)) or
+                        (torch.zeros(x8.shape[0], w1.shape[0] // 2, dtype=torch.int8),
+                         torch.ones(x8.shape[0], 1)))
+    monkeypatch.setattr(int8_linear, "_int8_linear_prequant",
+                        lambda x8, xs, w, ws, b, dt, shape, split_tail=False: ("fc2", shape, split_tail))
+    K, F, N2 = 64, 256, 32
+    x = torch.zeros(70, K, dtype=torch.bfloat16)
+    fc1 = _layer(FakeQT(_i8((2 * F, K), 1), torch.rand(2 * F)))
+    fc2 = _layer(FakeQT(_i8((N2, F), 2), torch.rand(N2), convrot=True))
+    f = int8_linear.int8_mlp_bridge
+    assert f(fc1, fc2, x) == ("fc2", (70, K), True) and seen == [(2 * F, K)]
+    assert f(fc1, _layer(FakeQT(_i8((N2, F), 2), torch.rand(N2))), x) is None    # FC2 not ConvRot
+    assert f(fc1, fc2, x.float()) is None
+    assert f(_layer(FakeQT(_i8((2 * F, K), 1), torch.rand(1))), fc2, x) is None   # per-tensor FC1
+    assert f(_layer(FakeQT(_i8((3 * F, K), 1), torch.rand(3 * F))), fc2, x) is None
+    lora = _layer(FakeQT(_i8((2 * F, K), 1), torch.rand(2 * F)))
+    lora._asfp8_runtime_lora = object()
+    assert f(lora, fc2, x) is None
+    monkeypatch.setenv("C4Q_INT8_MLP_BRIDGE", "0")
+    assert f(fc1, fc2, x) is None
 
 
 def test_swiglu_forward_routes(cpu_gate, monkeypatch):
