@@ -10,11 +10,11 @@ TFLOP/s (2*M*K*N per linear). ``roofline`` covers the dominant kernel of
 that step (the QKV W8A16 GEMM: one launch of whole rounds of 256x256 tiles
 plus one launch of the leftover tiles as split-K 64x64 pieces), timed with HIP
 events around each QKV call inside the timed region. ``per_config`` adds C1, C3, C4 and C5
-measured in the same process, plus MOSS_BF16, WAN_FP16, CONVROT and H3_QKV
-(the bf16 FC1/SiTU pair, the fp16-output INT8 epilogue, the fused head-merge
-+ ConvRot + quant pass and the SwiGLU + ConvRot pass, the INT8 QKV projection
-into the attention layout with and without Q/K RMSNorm + RoPE; not BASELINE
-configs); ``cpu_baseline`` times the reference's
+measured in the same process, plus MOSS_BF16, WAN_FP16, CONVROT and H3 (the
+bf16 FC1/SiTU pair, the fp16-output INT8 epilogue, the fused head-merge +
+ConvRot + quant pass and the SwiGLU + ConvRot pass, the H3 INT8 QKV
+projection into the attention layout with and without Q/K RMSNorm + RoPE and
+the H3 MLP bridge; not BASELINE configs); ``cpu_baseline`` times the reference's
 PyTorch CPU path for C2 (kitchen dequant + bf16 F.linear) on a bounded row
 sample on this host's cores.
 
@@ -319,12 +319,13 @@ def bench_convrot(torch, ops, dev, steps, warmup):
     return res
 
 
-def bench_h3_qkv(torch, ops, dev, steps, warmup):
-    """H3 INT8 QKV projection (56 heads of 128, hidden 5376; 8192 tokens)
-    into the attention layout: the plain per-channel epilogue, the QKV
+def bench_h3(torch, ops, dev, steps, warmup):
+    """H3 INT8 projections at 8192 tokens (hidden 5376). QKV (56 heads of
+    128) into the attention layout: the plain per-channel epilogue, the QKV
     scatter, and the scatter + Q/K RMSNorm + partial RoPE (R = 48) on its
     default route (scatter, then the in-place norm/RoPE pass) and on the
-    fused-epilogue route (C4Q_QKV_NORM_FUSE=1)."""
+    fused-epilogue route (C4Q_QKV_NORM_FUSE=1). MLP: FC1 (28672 wide) alone
+    and the bridge FC1 -> SwiGLU -> ConvRot -> rowwise quant."""
     import os
     M, H, K, R = 8192, 56, 5376, 48
     N = 3 * H * 128
@@ -357,6 +358,21 @@ def bench_h3_qkv(torch, ops, dev, steps, warmup):
         del os.environ["C4Q_QKV_NORM_FUSE"]
     res["qkv_rms_rope_fused_epilogue"] = {"us": kern * 1e6, "tops": ops_ / kern / 1e12,
                                           "frac_int8_peak": ops_ / kern / 1e12 / PEAK["int8"]}
+    del a, b, rs, cs, bias, fr
+    # FC1 -> SwiGLU -> ConvRot -> rowwise quant (the MLP bridge's front half),
+    # FC1 [8192, 5376] x [28672, 5376]; TOPS count FC1's MACs only
+    W = 28672
+    a = torch.randint(-128, 128, (M, K), generator=g, device=dev, dtype=torch.int8)
+    w1 = torch.randint(-128, 128, (W, K), generator=g, device=dev, dtype=torch.int8)
+    rs = torch.rand(M, generator=g, device=dev) * 0.01
+    cs = torch.rand(W, generator=g, device=dev) * 0.002
+    bias = torch.randn(W, generator=g, device=dev).to(torch.bfloat16)
+    fl = 2.0 * M * K * W
+    for name, fn in (("fc1_fused_cs", lambda: ops.i8_matmul2d_nt_fused_cs(a, w1, rs, cs, bias)),
+                     ("mlp_bridge_prequant", lambda: ops.i8_mlp_bridge_prequant(a, w1, rs, cs, bias))):
+        _, kern = Timer(torch).run(lambda p: marked(p, fn), max(5, steps // 2), max(2, warmup // 2))
+        res[name] = {"us": kern * 1e6, "tops": fl / kern / 1e12,
+                     "frac_int8_peak": fl / kern / 1e12 / PEAK["int8"], "shape": [M, K, W]}
     return res
 
 
@@ -503,9 +519,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--only", default="C1,C2,C3,C4,C5,MOSS_BF16,WAN_FP16,CONVROT,H3_QKV",
+    ap.add_argument("--only", default="C1,C2,C3,C4,C5,MOSS_BF16,WAN_FP16,CONVROT,H3",
                     help="comma list of configs to run (C2 is always run); MOSS_BF16, "
-                         "WAN_FP16, CONVROT and H3_QKV time the widened rows (not BASELINE configs)")
+                         "WAN_FP16, CONVROT and H3 time the widened rows (not BASELINE configs)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--pmc-target", action="store_true",
                     help="run the copy calibration and the C2 QKV kernel for rocprofv3 --pmc")
@@ -535,7 +551,7 @@ def main():
     torch.cuda.empty_cache()
     for name, fn in (("C1", bench_c1), ("C3", bench_c3), ("C4", bench_c4), ("C5", bench_c5),
                      ("MOSS_BF16", bench_moss_bf16), ("WAN_FP16", bench_wan_fp16),
-                     ("CONVROT", bench_convrot), ("H3_QKV", bench_h3_qkv)):
+                     ("CONVROT", bench_convrot), ("H3", bench_h3)):
         if name in only:
             log(f"{name} ...")
             per[name] = fn(torch, ops, dev, args.steps, args.warmup)

@@ -255,10 +255,13 @@ def i8_matmul2d_nt_fused_cs_qkv_rms_rope(a_i8, b_i8, row_scale, col_scale, bias,
     return outs
 
 
-# Chunk of FC1 rows of the MLP bridge when the caller asks for "auto": the
-# bf16 FC1 chunk and its rotated half stay in the Infinity Cache between the
-# three passes (H3 W = 28672: 2048 rows are 117 + 59 MB).
-MLP_BRIDGE_AUTO_ROWS = 2048
+# Chunk of FC1 rows of the MLP bridge when the caller asks for "auto": all
+# of them. Measured on MI355X at H3's FC1 (K 5376, W 28672), whole-M FC1
+# GEMMs win over chunks whose bf16 output would stay in the Infinity Cache:
+# 8192 rows take 1344 us at once, 1364 in chunks of 4096, 1536 of 2048, 1512
+# of 1024 (5378 rows: 964 / 972 / 1009 / 1006). The scratch then holds the
+# whole [M, 2F] FC1 output (470 MB at 8192 rows), small against 288 GB HBM.
+MLP_BRIDGE_AUTO_ROWS = 0
 
 
 def i8_mlp_bridge_prequant(a_i8, fc1_weight, row_scale, fc1_col_scale, fc1_bias=None,
@@ -282,7 +285,9 @@ def i8_mlp_bridge_prequant(a_i8, fc1_weight, row_scale, fc1_col_scale, fc1_bias=
     _vec(row_scale, M, torch.float32, "row_scale")
     _vec(fc1_col_scale, W, torch.float32, "fc1_col_scale")
     bias = _bias_bf16(fc1_bias, W)
-    rows = M if tile_rows == 0 else min(M, MLP_BRIDGE_AUTO_ROWS if tile_rows < 0 else tile_rows)
+    if tile_rows < 0:
+        tile_rows = MLP_BRIDGE_AUTO_ROWS
+    rows = M if tile_rows == 0 else min(M, tile_rows)
     rows = rows // 128 * 128 if rows >= 128 else rows
     F = W // 2
     wide = torch.empty((rows, W), dtype=torch.bfloat16, device=dev)
