@@ -252,17 +252,25 @@ extern "C" int c4q_i8_mlp_bridge_prequant(const int8_t* a, int64_t lda, const in
               "%s: need W = 2F > 0 with F a multiple of 256 (W=%lld)", what, (long long)W);
   C4Q_REQUIRE(tile_rows > 0, C4Q_ERR_SHAPE, "%s: tile_rows must be positive", what);
   if (M == 0) return C4Q_OK;
-  C4Q_REQUIRE(wide && rot && q && scales && silu_table, C4Q_ERR_ARG, "%s: null buffer", what);
+  C4Q_REQUIRE(wide && q && scales && silu_table, C4Q_ERR_ARG, "%s: null buffer", what);
   const int64_t F = W / 2;
-  // per chunk of rows: FC1 with the per-channel epilogue into `wide`, the
-  // SwiGLU + ConvRot pass into `rot`, rowwise quant into the chunk's q rows
+  // rows of F <= 15360 fit the one-pass SwiGLU + ConvRot + quant (the
+  // rotated row stays in LDS); wider rows go through `rot`
+  const bool one_pass = F * 2 <= 30 * 1024;
+  C4Q_REQUIRE(one_pass || rot != nullptr, C4Q_ERR_ARG, "%s: null rot scratch", what);
+  // per chunk of rows: FC1 with the per-channel epilogue into `wide`, then
+  // SwiGLU + ConvRot + rowwise quant into the chunk's q rows
   for (int64_t r0 = 0; r0 < M; r0 += tile_rows) {
     const int64_t rows = M - r0 < tile_rows ? M - r0 : tile_rows;
     int st = c4q_i8_gemm_nt_fused_cs(a + r0 * lda, lda, w1, ldw, wide, W, row_scale + r0, col_scale,
                                      bias, rows, W, K, stream);
-    if (st == C4Q_OK) st = c4q_i8_swiglu_rot(wide, rows, F, silu_table, rot, stream);
-    if (st == C4Q_OK)
-      st = c4q_i8_quant_rowwise(rot, C4Q_BF16, F, q + r0 * F, F, scales + r0, rows, F, stream);
+    if (st == C4Q_OK && one_pass)
+      st = c4q_i8_swiglu_rot_quant(wide, rows, F, silu_table, q + r0 * F, scales + r0, stream);
+    if (st == C4Q_OK && !one_pass) {
+      st = c4q_i8_swiglu_rot(wide, rows, F, silu_table, rot, stream);
+      if (st == C4Q_OK)
+        st = c4q_i8_quant_rowwise(rot, C4Q_BF16, F, q + r0 * F, F, scales + r0, rows, F, stream);
+    }
     if (st != C4Q_OK) return st;
   }
   return C4Q_OK;

@@ -211,6 +211,36 @@ __device__ __forceinline__ void rot_group16(float (&v)[16], float* slot, int c, 
   lds_fence_wave();                                         // slot free again
 }
 
+// Rowwise quant of a bf16 row held in LDS (256 threads, after the barrier
+// that produced amax): the i8_quant_rowwise arithmetic, 16-byte stores of
+// 16 codes per thread where q is aligned (K is a multiple of 256).
+__device__ __forceinline__ void quant_row_from_lds(const uint16_t* rot, int K, float amax, int8_t* qr,
+                                                   float* scale_out, int vec_q) {
+  const int tid = threadIdx.x;
+  const float scale = fmaxf(amax / 127.0f, 1e-30f);
+  if (tid == 0) *scale_out = scale;
+  float sc = round_half(scale, true);
+  if (sc == 0.0f) sc = 1.1754943508222875e-38f;
+  const float rc = 1.0f / sc;
+  if (vec_q) {
+    for (int i = tid * 16; i < K; i += 4096) {
+      const uint4 lo = *reinterpret_cast<const uint4*>(rot + i);
+      const uint4 hi = *reinterpret_cast<const uint4*>(rot + i + 8);
+      const uint32_t h16[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+      uint32_t out[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        out[c] = quant_i8<true>((uint16_t)h16[2 * c], sc, rc) |
+                 (quant_i8<true>((uint16_t)(h16[2 * c] >> 16), sc, rc) << 8) |
+                 (quant_i8<true>((uint16_t)h16[2 * c + 1], sc, rc) << 16) |
+                 (quant_i8<true>((uint16_t)(h16[2 * c + 1] >> 16), sc, rc) << 24);
+      *reinterpret_cast<uint4*>(qr + i) = uint4{out[0], out[1], out[2], out[3]};
+    }
+  } else {
+    for (int i = tid; i < K; i += 256) qr[i] = (int8_t)quant_i8<true>(rot[i], sc, rc);
+  }
+}
+
 template <bool ROTATE>
 __global__ void __launch_bounds__(256)
 merge_rot_quant_kernel(const uint16_t* x, int64_t H, int64_t S, int64_t D, int8_t* q,
@@ -274,29 +304,7 @@ merge_rot_quant_kernel(const uint16_t* x, int64_t H, int64_t S, int64_t D, int8_
     }
   }
   const float amax = block_max256(mx, red);    // its barrier also publishes the rotated row
-  const float scale = fmaxf(amax / 127.0f, 1e-30f);
-  if (tid == 0) scales[row] = scale;
-  float sc = round_half(scale, true);
-  if (sc == 0.0f) sc = 1.1754943508222875e-38f;
-  const float rc = 1.0f / sc;
-  int8_t* qr = q + row * (int64_t)K;
-  if (vec_q) {
-    for (int i = tid * 16; i < K; i += 4096) {
-      const uint4 lo = *reinterpret_cast<const uint4*>(rot + i);
-      const uint4 hi = *reinterpret_cast<const uint4*>(rot + i + 8);
-      const uint32_t h16[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-      uint32_t out[4];
-#pragma unroll
-      for (int c = 0; c < 4; ++c)
-        out[c] = quant_i8<true>((uint16_t)h16[2 * c], sc, rc) |
-                 (quant_i8<true>((uint16_t)(h16[2 * c] >> 16), sc, rc) << 8) |
-                 (quant_i8<true>((uint16_t)h16[2 * c + 1], sc, rc) << 16) |
-                 (quant_i8<true>((uint16_t)(h16[2 * c + 1] >> 16), sc, rc) << 24);
-      *reinterpret_cast<uint4*>(qr + i) = uint4{out[0], out[1], out[2], out[3]};
-    }
-  } else {
-    for (int i = tid; i < K; i += 256) qr[i] = (int8_t)quant_i8<true>(rot[i], sc, rc);
-  }
+  quant_row_from_lds(rot, K, amax, q + row * (int64_t)K, scales + row, vec_q);
 }
 
 // SwiGLU + ConvRot pre-pass of an H3 INT8 fc2 (reference i8_swiglu_rot_bf16,
@@ -353,6 +361,59 @@ swiglu_rot_kernel(const uint16_t* x, int64_t F, const uint16_t* silu, uint16_t* 
     }
     lds_fence_wave();
   }
+}
+
+// The SwiGLU + ConvRot pass and the rowwise quant of its rows in one pass
+// (the MLP bridge's second and third steps without the bf16 row in HBM):
+// x [M, 2F] bf16 -> q [M, F] int8 and scales [M], the bytes of
+// i8_quant_rowwise(swiglu_rot(x)). One workgroup per row; the rotated row
+// (F bf16, F <= 15360) is kept in LDS for the quant, as in
+// merge_rot_quant_kernel.
+__global__ void __launch_bounds__(256)
+swiglu_rot_quant_kernel(const uint16_t* x, int64_t F, const uint16_t* silu, int8_t* q,
+                        float* scales, int vec_q) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t rot[];   // the rotated row, F bf16
+  __shared__ __attribute__((aligned(16))) float work[4][4 * kRotSlot];
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const uint16_t* xr = x + row * 2 * F;
+  const int groups = (int)(F >> 8);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int gq = lane >> 4, c = lane & 15;
+  float* slot = work[wave] + gq * kRotSlot;
+  float mx = 0.0f;
+  for (int g0 = wave * 4; g0 < groups; g0 += 16) {
+    const int g = g0 + gq;
+    const bool live = g < groups;
+    float v[16];
+    if (live) {
+      const uint16_t* ga = xr + g * 256 + 16 * c;
+      const uint4 a0 = *reinterpret_cast<const uint4*>(ga);
+      const uint4 a1 = *reinterpret_cast<const uint4*>(ga + 8);
+      const uint4 b0 = *reinterpret_cast<const uint4*>(ga + F);
+      const uint4 b1 = *reinterpret_cast<const uint4*>(ga + F + 8);
+      const uint32_t wa[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+      const uint32_t wb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const float s0 = bf16_f32(silu[wa[k] & 0xFFFFu]), s1 = bf16_f32(silu[wa[k] >> 16]);
+        const uint32_t p = bf16x2_rne(s0 * bf16lo(wb[k]), s1 * bf16hi(wb[k]));
+        v[2 * k] = bf16lo(p);
+        v[2 * k + 1] = bf16hi(p);
+      }
+    }
+    rot_group16(v, slot, c, live);
+    if (live) {
+      uint16_t* grp = rot + g * 256;
+#pragma unroll
+      for (int m = 0; m < 16; ++m) {
+        grp[c + 16 * m] = (uint16_t)(f32_bits(v[m]) >> 16);
+        mx = fmaxf(mx, fabsf(v[m]));
+      }
+    }
+  }
+  const float amax = block_max256(mx, red);    // its barrier also publishes the rotated row
+  quant_row_from_lds(rot, (int)F, amax, q + row * F, scales + row, vec_q);
 }
 
 __global__ void fill_zero_kernel(float* p) { p[0] = 0.0f; }
@@ -537,6 +598,22 @@ extern "C" int c4q_i8_swiglu_rot(const uint16_t* x, int64_t M, int64_t F,
               what);
   hipLaunchKernelGGL(swiglu_rot_kernel, dim3((unsigned)M), dim3(256), 0, as_stream(stream), x, F,
                      silu_table, rot);
+  return check_launch(what);
+}
+
+extern "C" int c4q_i8_swiglu_rot_quant(const uint16_t* x, int64_t M, int64_t F,
+                                       const uint16_t* silu_table, int8_t* q, float* scales,
+                                       void* stream) {
+  const char* what = "c4q_i8_swiglu_rot_quant";
+  C4Q_REQUIRE(M >= 0 && F >= 0 && F % 256 == 0 && F * 2 <= 30 * 1024, C4Q_ERR_SHAPE,
+              "%s: need F a multiple of 256, at most 15360 (M=%lld F=%lld)", what, (long long)M,
+              (long long)F);
+  if (M == 0 || F == 0) return C4Q_OK;
+  C4Q_REQUIRE(M < (1ll << 31), C4Q_ERR_SHAPE, "%s: too many rows", what);
+  C4Q_REQUIRE(x && q && scales && silu_table, C4Q_ERR_ARG, "%s: null pointer", what);
+  C4Q_REQUIRE(aligned16(x), C4Q_ERR_ARG, "%s: x must be 16-byte aligned", what);
+  hipLaunchKernelGGL(swiglu_rot_quant_kernel, dim3((unsigned)M), dim3(256), (size_t)F * 2,
+                     as_stream(stream), x, F, silu_table, q, scales, (int)aligned16(q));
   return check_launch(what);
 }
 

@@ -291,7 +291,8 @@ def i8_mlp_bridge_prequant(a_i8, fc1_weight, row_scale, fc1_col_scale, fc1_bias=
     rows = rows // 128 * 128 if rows >= 128 else rows
     F = W // 2
     wide = torch.empty((rows, W), dtype=torch.bfloat16, device=dev)
-    rot = torch.empty((rows, F), dtype=torch.bfloat16, device=dev)
+    # rows of F <= 15360 are rotated and quantized in one pass (no rot scratch)
+    rot = torch.empty((rows, F) if F * 2 > 30 * 1024 else (0,), dtype=torch.bfloat16, device=dev)
     q = torch.empty((M, F), dtype=torch.int8, device=dev)
     scales = torch.empty((M, 1), dtype=torch.float32, device=dev)
     silu = act_table("silu", dev)
@@ -299,7 +300,8 @@ def i8_mlp_bridge_prequant(a_i8, fc1_weight, row_scale, fc1_col_scale, fc1_bias=
         _lib.call("c4q_i8_mlp_bridge_prequant", a_i8.data_ptr(), lda, fc1_weight.data_ptr(), ldw,
                   row_scale.data_ptr(), fc1_col_scale.data_ptr(),
                   bias.data_ptr() if bias is not None else None, silu.data_ptr(), M, K, W, rows,
-                  wide.data_ptr(), rot.data_ptr(), q.data_ptr(), scales.data_ptr(), _stream(dev))
+                  wide.data_ptr(), rot.data_ptr() if rot.numel() else None, q.data_ptr(),
+                  scales.data_ptr(), _stream(dev))
     return q, scales
 
 

@@ -145,14 +145,23 @@ int c4q_i8_merge_rot_quant(const uint16_t* x, int64_t B, int64_t H, int64_t S, i
 int c4q_i8_swiglu_rot(const uint16_t* x, int64_t M, int64_t F, const uint16_t* silu_table,
                       uint16_t* rot, void* stream);
 
+/* SwiGLU + ConvRot + rowwise quant in one pass: x [M, 2F] bf16 (16-byte
+ * aligned) -> q [M, F] int8 contiguous and scales [M] fp32, the bytes of
+ * c4q_i8_quant_rowwise(c4q_i8_swiglu_rot(x)); F a multiple of 256, at most
+ * 15360. Replaces the reference bridge's i8_swiglu_rot_max_inplace_bf16 +
+ * i8_quant_rowwise_premax_strided_bf16 pair (_patches/int8_ext/int8_gemm.mm:1249-1330). */
+int c4q_i8_swiglu_rot_quant(const uint16_t* x, int64_t M, int64_t F, const uint16_t* silu_table,
+                            int8_t* q, float* scales, void* stream);
+
 /* H3 FC1/SwiGLU/FC2 bridge, front half: FC2's ConvRot-rotated, rowwise-
- * quantized activation from FC1's int8 input, FC1 [M, W] never stored
- * whole. Per chunk of tile_rows rows: wide = c4q_i8_gemm_nt_fused_cs(a rows,
- * w1 [W, K], row_scale rows, col_scale [W], bias [W] or NULL) as bf16
- * [rows, W]; rot = c4q_i8_swiglu_rot(wide) [rows, F], F = W/2 a multiple of
- * 256; q rows [rows, F] int8 and scales rows = c4q_i8_quant_rowwise(rot).
- * wide (tile_rows x W bf16) and rot (tile_rows x F bf16) are the caller's
- * scratch, 16-byte aligned; q [M, F] contiguous, scales [M]. Replaces
+ * quantized activation from FC1's int8 input. Per chunk of tile_rows rows:
+ * wide = c4q_i8_gemm_nt_fused_cs(a rows, w1 [W, K], row_scale rows,
+ * col_scale [W], bias [W] or NULL) as bf16 [rows, W], F = W/2 a multiple
+ * of 256; then q rows [rows, F] int8 and scales rows =
+ * c4q_i8_swiglu_rot_quant(wide) (F <= 15360), or c4q_i8_swiglu_rot into rot
+ * [rows, F] followed by c4q_i8_quant_rowwise (wider F). wide (tile_rows x W
+ * bf16) and rot (tile_rows x F bf16; may be NULL when F <= 15360) are the
+ * caller's scratch, 16-byte aligned; q [M, F] contiguous, scales [M]. Replaces
  * i8_mlp_bridge_prequant (_patches/int8_ext/int8_gemm.mm:2377-2537) behind
  * int8_mlp_bridge (_patches/int8_linear_kernel_mps.py:538-673). */
 int c4q_i8_mlp_bridge_prequant(const int8_t* a, int64_t lda, const int8_t* w1, int64_t ldw,

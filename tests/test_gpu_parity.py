@@ -413,11 +413,13 @@ def test_i8_fused_cs_qkv_rms_rope_rejects_bad_shapes(dev):
 
 @pytest.mark.parametrize("M,K,F,tile_rows", [(300, 512, 256, -1), (1000, 256, 512, 128),
                                               (1000, 256, 512, 200), (700, 128, 256, 0),
-                                              (2500, 384, 256, -1)])
+                                              (2500, 384, 256, -1), (90, 128, 15360, -1),
+                                              (100, 128, 15616, 0)])
 def test_i8_mlp_bridge_prequant_exact(dev, M, K, F, tile_rows):
     """FC1 -> SwiGLU -> ConvRot -> rowwise quant, chunk by chunk: the bytes of
     the unfused oracle chain for every chunking (auto, 128-row chunks, 200
-    rounded down to 128, all rows at once; ragged last chunks)."""
+    rounded down to 128, all rows at once; ragged last chunks), through the
+    one-pass rotate + quant (F <= 15360) and the two-pass route (F 15616)."""
     g = gen(5 + M + F)
     W = 2 * F
     a, w1 = _randint8((M, K), g), _randint8((W, K), g)
