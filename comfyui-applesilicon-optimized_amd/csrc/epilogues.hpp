@@ -281,12 +281,18 @@ __device__ __forceinline__ float sum8_lanes(float v) {
 __device__ __forceinline__ void head_rms_norm(const float (&x)[16], const float (&w)[16], float eps,
                                               float (&y)[16]) {
   float ss = 0.0f;
+  // x * x is exact in f32 (x is a bf16 value), so the fused multiply-add
+  // rounds exactly like ss + x * x
 #pragma unroll
-  for (int k = 0; k < 16; ++k) ss = ss + x[k] * x[k];
+  for (int k = 0; k < 16; ++k) ss = __builtin_fmaf(x[k], x[k], ss);
   ss = sum8_lanes(ss);
   const float inv = 1.0f / __builtin_sqrtf(ss * 0.0078125f + eps);
 #pragma unroll
-  for (int k = 0; k < 16; ++k) y[k] = round_bf16((x[k] * inv) * w[k]);
+  for (int k = 0; k < 16; k += 2) {
+    const uint32_t p = bf16x2_rne((x[k] * inv) * w[k], (x[k + 1] * inv) * w[k + 1]);
+    y[k] = bf16lo(p);
+    y[k + 1] = bf16hi(p);
+  }
 }
 
 // Split-half RoPE of column d < 2R (reference int8_gemm.mm:843-854, the

@@ -113,17 +113,22 @@ namespace {
 // does not apply (R not a multiple of 8, or operands the tiled kernels
 // cannot take), with the lane map and arithmetic of epilogue_head_norm (8
 // rows per wave: lane l holds row l/8, columns 64 h + 8 (l%8) + k). Rows
-// run token-major -- row r is token m = r / 2H, kind (r / H) % 2, head r % H
-// -- so the 2H rows that share a token's freqs row run together. A row is
-// read whole before any lane writes it.
+// are taken 8 consecutive tokens of one (kind, head) per wave, chunk by
+// chunk of 8 tokens, so the 2H waves of a chunk read its freqs rows from
+// the cache. A row is read whole before any lane writes it.
+template <bool UNITS>
 __global__ void __launch_bounds__(256) head_norm_rope_kernel(EpiQKVNormRope epi, int64_t H) {
   using St = Strip<128>;
   using Map = StoreMap<128, uint16_t>;
-  __shared__ float rows[4][St::kBytes / 4];
+  __shared__ __attribute__((aligned(16))) float rows[4][St::kBytes / 4];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, prow = lane >> 3;
-  const int64_t r = ((int64_t)blockIdx.x * 4 + wave) * 8 + prow;
-  const bool live = r < 2 * H * epi.rows;
-  const int64_t m = r / (2 * H), t = r - m * 2 * H;
+  // wave w covers 8 consecutive tokens of one (kind, head) row set: chunk
+  // c of 8 tokens, then (kind, head) t -- a wave reads 2 KB contiguous, and
+  // the 2H waves of a chunk share its 8 freqs rows through the cache
+  const int64_t wv = (int64_t)blockIdx.x * 4 + wave;
+  const int64_t c8 = wv / (2 * H), t = wv - c8 * 2 * H;
+  const int64_t m = c8 * 8 + prow;
+  const bool live = m < epi.rows;
   const uint32_t kind = t >= H ? 1u : 0u;
   const int64_t hd = t - (int64_t)kind * H;
   uint8_t* row = static_cast<uint8_t*>(epi.d) + epi.koff * (int64_t)kind + (hd * epi.rows + m) * 256;
@@ -146,29 +151,69 @@ __global__ void __launch_bounds__(256) head_norm_rope_kernel(EpiQKVNormRope epi,
       w[8 * h + k] = f.x; w[8 * h + k + 1] = f.y; w[8 * h + k + 2] = f.z; w[8 * h + k + 3] = f.w;
     }
   }
+  const int R = epi.pairs;
+  const uint8_t* frow = reinterpret_cast<const uint8_t*>(epi.freqs) + (live ? m : 0) * R * 8;
+  uint32_t fw[16];
+  int pc[2];
+  uint32_t swap[2];
+  bool pass[2];
+  if constexpr (UNITS) {
+    // R % 8 == 0: each 8-column unit lies in one rotation half or past 2R;
+    // its freqs words load with constant offsets (see epilogue_head_norm)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int c0 = Map::col(lane, 2 * h);
+      const bool first = c0 < R, second = !first && c0 < 2 * R;
+      pass[h] = !first && !second;
+      pc[h] = first ? c0 + R : (second ? c0 - R : c0);
+      swap[h] = second ? 16u : 0u;
+      if (live && !pass[h]) {
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(
+            frow + (first ? 8 * c0 : 8 * (c0 - R) + 4));
+#pragma unroll
+        for (int k = 0; k < 8; ++k) fw[8 * h + k] = p[2 * k];
+      }
+    }
+  }
   head_rms_norm(x, w, epi.eps, y);
   float* sf = rows[wave];
 #pragma unroll
   for (int h = 0; h < 2; ++h)
 #pragma unroll
-    for (int k = 0; k < 8; ++k) sf[St::word(prow, Map::col(lane, 2 * h) + k)] = y[8 * h + k];
+    for (int k = 0; k < 8; k += 4)
+      *reinterpret_cast<float4*>(sf + St::word(prow, Map::col(lane, 2 * h) + k)) =
+          float4{y[8 * h + k], y[8 * h + k + 1], y[8 * h + k + 2], y[8 * h + k + 3]};
   lds_fence_wave();
   if (!live) return;
-  const int R = epi.pairs;
-  const uint32_t* fr = epi.freqs + m * R * 2;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const int c0 = Map::col(lane, 2 * h);
     float o[8];
+    if constexpr (UNITS) {
+      float yp[8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const int d = c0 + k;
-      o[k] = y[8 * h + k];
-      if (d < 2 * R) {
-        const bool second = d >= R;
-        const int ii = second ? d - R : d;
-        const float yp = sf[St::word(prow, second ? ii : d + R)];
-        o[k] = rope_split_half(o[k], yp, fr[2 * ii + (second ? 1 : 0)], second);
+      for (int k = 0; k < 8; k += 4) {
+        const float4 t4 = *reinterpret_cast<const float4*>(sf + St::word(prow, pc[h] + k));
+        yp[k] = t4.x; yp[k + 1] = t4.y; yp[k + 2] = t4.z; yp[k + 3] = t4.w;
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const uint32_t f = __builtin_amdgcn_alignbit(fw[8 * h + k], fw[8 * h + k], swap[h]);
+        const float rr = rope_split_half(y[8 * h + k], yp[k], f, false);
+        o[k] = pass[h] ? y[8 * h + k] : rr;
+      }
+    } else {
+      const uint32_t* fr = reinterpret_cast<const uint32_t*>(frow);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int d = c0 + k;
+        o[k] = y[8 * h + k];
+        if (d < 2 * R) {
+          const bool second = d >= R;
+          const int ii = second ? d - R : d;
+          const float yp = sf[St::word(prow, second ? ii : d + R)];
+          o[k] = rope_split_half(o[k], yp, fr[2 * ii + (second ? 1 : 0)], second);
+        }
       }
     }
     *reinterpret_cast<uint4*>(row + c0 * 2) =
@@ -235,9 +280,12 @@ extern "C" int c4q_i8_gemm_nt_fused_cs_qkv_rms_rope(
   st = tiled ? run_tiles<false>(M, N, N, K, sa, sb, nullptr, scatter, s, what, op_for)
              : launch_generic(M, N, K, GenI8::make(a8, lda, b8, ldb), scatter, s, what);
   if (st) return st;
-  const int64_t blocks = cdiv(2 * H * M, 32);
+  const int64_t blocks = cdiv(cdiv(M, 8) * 2 * H, 4);     // one wave per 8 tokens x (kind, head)
   C4Q_REQUIRE(blocks < (1ll << 31), C4Q_ERR_SHAPE, "%s: problem too large", what);
-  hipLaunchKernelGGL(head_norm_rope_kernel, dim3((unsigned)blocks), dim3(256), 0, s, epi, H);
+  if (R % 8 == 0)
+    hipLaunchKernelGGL(head_norm_rope_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, s, epi, H);
+  else
+    hipLaunchKernelGGL(head_norm_rope_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, s, epi, H);
   return check_launch(what);
 }
 
