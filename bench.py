@@ -16,7 +16,8 @@ ConvRot + quant pass and the SwiGLU + ConvRot pass, the H3 INT8 QKV
 projection into the attention layout with and without Q/K RMSNorm + RoPE and
 the H3 MLP bridge; not BASELINE configs); ``cpu_baseline`` times the reference's
 PyTorch CPU path for C2 (kitchen dequant + bf16 F.linear) on a bounded row
-sample on this host's cores.
+sample on this host's cores, and ``per_config`` C1 / C3 / C4 carry the same
+for those configs under "cpu".
 
 Inputs are synthetic, generated from fixed seeds directly in HBM before the
 timed region; weights are random-init N(0, 0.02) quantized the way each
@@ -137,14 +138,7 @@ def cpu_baseline_c2(torch, budget_s=12.0):
     sample of C2 sized for ~budget_s of CPU work; weights at full size."""
     sys.path.insert(0, str(ROOT))
     from oracle import torch_path
-    try:
-        cores = len(os.sched_getaffinity(0))
-    except AttributeError:
-        cores = os.cpu_count() or 1
-    env_cap = os.environ.get("OMP_NUM_THREADS")
-    if env_cap and env_cap.isdigit():
-        cores = min(cores, int(env_cap))
-    torch.set_num_threads(cores)
+    _cpu_cores(torch)
     K, Ns = 3072, (9216, 3072)
     g = torch.Generator().manual_seed(2)
     ws = []
@@ -183,6 +177,68 @@ def cpu_baseline_c2(torch, budget_s=12.0):
                    f"weights dequantized per call), median of {reps} reps = {tmed:.3f} s; "
                    f"torch CPU, {model}"),
     }
+
+
+def _cpu_cores(torch):
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count() or 1
+    env_cap = os.environ.get("OMP_NUM_THREADS")
+    if env_cap and env_cap.isdigit():
+        cores = min(cores, int(env_cap))
+    torch.set_num_threads(cores)
+    return cores
+
+
+def cpu_baseline_configs(torch, budget_s=4.0):
+    """The reference's CPU path (oracle/torch_path.py) for C1, C3 (up-proj)
+    and C4 on row samples of each config sized for ~budget_s of CPU work
+    apiece, weights at full size except C3's (a 512-row slice):
+    {config: {tops, rows, cols, reps, seconds_per_rep, cores}}."""
+    sys.path.insert(0, str(ROOT))
+    from oracle import torch_path as tp
+    cores = _cpu_cores(torch)
+    g = torch.Generator().manual_seed(12)
+    fp8 = torch.float8_e4m3fn
+
+    def i8(*shape):
+        return torch.randint(-127, 128, shape, generator=g, dtype=torch.int8)
+
+    cases = {}
+    w1 = i8(3072, 3072)
+    cs1 = 0.0005 + 0.0015 * torch.rand(3072, generator=g)
+    cases["C1"] = (3072, 3072, lambda rows: (lambda x=i8(rows, 3072),
+                   rs=0.005 + 0.015 * torch.rand(rows, generator=g): tp.c1_int8_linear(x, w1, rs, cs1)))
+    w3 = (0.02 * torch.randn(13824, 5120, generator=g) / 0.0003).clamp(-448, 448).to(fp8)
+    one = torch.tensor(1.0)
+    # torch's CPU fp8 _scaled_mm is slow (~0.3 GFLOP/s here): C3 samples
+    # 512 of the 13824 weight rows as well
+    w3s = w3[:512].contiguous()
+    cases["C3"] = (5120, 512, lambda rows: (lambda x=torch.randn(rows, 5120, generator=g).clamp(
+                   -448, 448).to(fp8): tp.c3_scaled_mm(x, w3s, one, torch.tensor(0.0003))))
+    wg, wu = i8(12288, 3072), i8(12288, 3072)
+    gs = 0.0005 + 0.0015 * torch.rand(12288, generator=g)
+    us = 0.0005 + 0.0015 * torch.rand(12288, generator=g)
+    cases["C4"] = (3072, 2 * 12288, lambda rows: (lambda q=i8(rows, 3072),
+                   rs=0.005 + 0.015 * torch.rand(rows, generator=g): tp.c4_ffn_pair(q, wg, wu, rs, gs, us)))
+    out = {}
+    for name, (K, N, make) in cases.items():
+        def run(rows):
+            fn = make(rows)
+            t0 = time.perf_counter()
+            fn()
+            return time.perf_counter() - t0
+        rows = 16
+        run(rows)                                   # warm-up
+        t = run(rows)
+        rows = int(min(8192, max(16, rows * (budget_s / 3.0) / max(t, 1e-3))))
+        rows -= rows % 16
+        times = [run(rows) for _ in range(3)]
+        tmed = statistics.median(times)
+        out[name] = {"tops": 2.0 * rows * K * N / tmed / 1e12, "rows": rows, "cols": N,
+                     "reps": 3, "seconds_per_rep": tmed, "cores": cores}
+    return out
 
 
 # ----------------------------------------------------------------- C1 ---
@@ -564,6 +620,14 @@ def main():
     if not args.no_cpu:
         log("CPU baseline (reference torch CPU path, C2 sample) ...")
         cpu = cpu_baseline_c2(torch)
+        log("CPU baselines of C1, C3, C4 (row samples) ...")
+        gpu_rate = {"C1": lambda d: d.get("tops"), "C3": lambda d: d.get("up", {}).get("tflops"),
+                    "C4": lambda d: d.get("tops")}
+        for name, c in cpu_baseline_configs(torch).items():
+            if name in per:
+                gr = gpu_rate[name](per[name])
+                c["gpu_over_cpu"] = gr / c["tops"] if gr and c["tops"] else None
+                per[name]["cpu"] = c
 
     kt = c2["kernel_tflops"]
     line = {

@@ -387,12 +387,13 @@ struct TileCoord { int tm, tn; };
 // Remap the dispatch order (blocks go round-robin over the 8 XCDs) so each
 // XCD owns a contiguous run of tiles, then raster that run in bands of
 // kGroupM tile rows.
-__host__ __device__ inline TileCoord tile_of(int bid, int nblocks, int tiles_m, int tiles_n) {
+__host__ __device__ inline TileCoord tile_of(int bid, int nblocks, int tiles_m, int tiles_n,
+                                             int group_m = kGroupM) {
   const int full = nblocks & ~7;
   if (bid < full) bid = (bid & 7) * (full >> 3) + (bid >> 3);
-  const int band = kGroupM * tiles_n;
-  const int first_m = (bid / band) * kGroupM;
-  const int gm = tiles_m - first_m < kGroupM ? tiles_m - first_m : kGroupM;
+  const int band = group_m * tiles_n;
+  const int first_m = (bid / band) * group_m;
+  const int gm = tiles_m - first_m < group_m ? tiles_m - first_m : group_m;
   const int in_band = bid - (bid / band) * band;
   TileCoord t;
   t.tm = first_m + in_band % gm;
@@ -411,6 +412,7 @@ struct GemmShape {
   int tiles_m, tiles_n;     // grid of mapped tiles
   int first, count;
   int sub_m, sub_n;
+  int group_m = kGroupM;    // tile rows per raster band
 };
 
 // Kernel tile i of a launch, in kernel-tile units. Split tiles: the
@@ -418,12 +420,13 @@ struct GemmShape {
 // kernel tiles, so the pieces of one mapped tile share an L2.
 __host__ __device__ inline TileCoord tile_at(const GemmShape& sh, int i) {
   const int nmapped = sh.tiles_m * sh.tiles_n;
-  if (sh.sub_m == 1 && sh.sub_n == 1) return tile_of(sh.first + i, nmapped, sh.tiles_m, sh.tiles_n);
+  if (sh.sub_m == 1 && sh.sub_n == 1)
+    return tile_of(sh.first + i, nmapped, sh.tiles_m, sh.tiles_n, sh.group_m);
   const int full = sh.count & ~7;
   if (i < full) i = (i & 7) * (full >> 3) + (i >> 3);
   const int per = sh.sub_m * sh.sub_n;
   const int t = i / per, s = i - t * per;
-  const TileCoord b = tile_of(sh.first + t, nmapped, sh.tiles_m, sh.tiles_n);
+  const TileCoord b = tile_of(sh.first + t, nmapped, sh.tiles_m, sh.tiles_n, sh.group_m);
   TileCoord r;
   r.tm = b.tm * sh.sub_m + s / sh.sub_n;
   r.tn = b.tn * sh.sub_n + s % sh.sub_n;

@@ -261,6 +261,11 @@ inline int plan_launches(int64_t M, int64_t n_rows_b, int64_t N, int64_t K, int 
   const int bm = Set::bm(p.main_id), bn = Set::bn(p.main_id);
   const int64_t mapped = cdiv(M, bm) * cdiv(n_rows_b, bn);
   GemmShape sh{M, N, K, (int)cdiv(M, bm), (int)cdiv(n_rows_b, bn), 0, (int)p.main_count, 1, 1};
+  const char* gm_env = getenv("C4Q_GROUP_M");          // raster band height, for sweeps
+  if (gm_env) {
+    const int gm = atoi(gm_env);
+    if (gm >= 1 && gm <= 64) sh.group_m = gm;
+  }
   int n = 0;
   if (sh.count > 0) {
     ids[n] = p.main_id;
