@@ -109,9 +109,8 @@ extern "C" int c4q_i8_gemm_nt_fused_cs_qkv(const int8_t* a, int64_t lda, const i
 namespace {
 
 // In-place Q/K RMSNorm + partial RoPE over the attention layout [1, H, M,
-// 128] of Q and K: the pass after the QKV scatter where the fused epilogue
-// does not apply (R not a multiple of 8, or operands the tiled kernels
-// cannot take), with the lane map and arithmetic of epilogue_head_norm (8
+// 128] of Q and K: the second pass of the two-pass route (after the QKV
+// scatter), with the lane map and arithmetic of epilogue_head_norm (8
 // rows per wave: lane l holds row l/8, columns 64 h + 8 (l%8) + k). Rows
 // are taken 8 consecutive tokens of one (kind, head) per wave, chunk by
 // chunk of 8 tokens, so the 2H waves of a chunk read its freqs rows from
@@ -125,12 +124,13 @@ __global__ void __launch_bounds__(256) head_norm_rope_kernel(EpiQKVNormRope epi,
   // wave w covers 8 consecutive tokens of one (kind, head) row set: chunk
   // c of 8 tokens, then (kind, head) t -- a wave reads 2 KB contiguous, and
   // the 2H waves of a chunk share its 8 freqs rows through the cache
-  const int64_t wv = (int64_t)blockIdx.x * 4 + wave;
-  const int64_t c8 = wv / (2 * H), t = wv - c8 * 2 * H;
-  const int64_t m = c8 * 8 + prow;
+  const uint32_t wv = blockIdx.x * 4u + (uint32_t)wave;   // < 2^31 (checked by the host)
+  const uint32_t h2 = (uint32_t)(2 * H);
+  const uint32_t c8 = wv / h2, t = wv - c8 * h2;
+  const int64_t m = (int64_t)c8 * 8 + prow;
   const bool live = m < epi.rows;
-  const uint32_t kind = t >= H ? 1u : 0u;
-  const int64_t hd = t - (int64_t)kind * H;
+  const uint32_t kind = t >= (uint32_t)H ? 1u : 0u;
+  const int64_t hd = (int64_t)(t - kind * (uint32_t)H);
   uint8_t* row = static_cast<uint8_t*>(epi.d) + epi.koff * (int64_t)kind + (hd * epi.rows + m) * 256;
   const float* wp = epi.weight(kind);
   float x[16], w[16], y[16];
@@ -197,10 +197,16 @@ __global__ void __launch_bounds__(256) head_norm_rope_kernel(EpiQKVNormRope epi,
         yp[k] = t4.x; yp[k + 1] = t4.y; yp[k + 2] = t4.z; yp[k + 3] = t4.w;
       }
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const uint32_t f = __builtin_amdgcn_alignbit(fw[8 * h + k], fw[8 * h + k], swap[h]);
-        const float rr = rope_split_half(y[8 * h + k], yp[k], f, false);
-        o[k] = pass[h] ? y[8 * h + k] : rr;
+      for (int k = 0; k < 8; k += 2) {
+        // rope_split_half for two columns, their diagonal products rounded
+        // by one paired conversion (the final rounding is the store's)
+        const uint32_t f0 = __builtin_amdgcn_alignbit(fw[8 * h + k], fw[8 * h + k], swap[h]);
+        const uint32_t f1 = __builtin_amdgcn_alignbit(fw[8 * h + k + 1], fw[8 * h + k + 1], swap[h]);
+        const uint32_t dp = bf16x2_rne(bf16lo(f0) * y[8 * h + k], bf16lo(f1) * y[8 * h + k + 1]);
+        const float r0 = bf16lo(dp) + bf16hi(f0) * yp[k];
+        const float r1 = bf16hi(dp) + bf16hi(f1) * yp[k + 1];
+        o[k] = pass[h] ? y[8 * h + k] : r0;
+        o[k + 1] = pass[h] ? y[8 * h + k + 1] : r1;
       }
     } else {
       const uint32_t* fr = reinterpret_cast<const uint32_t*>(frow);
@@ -281,7 +287,7 @@ extern "C" int c4q_i8_gemm_nt_fused_cs_qkv_rms_rope(
              : launch_generic(M, N, K, GenI8::make(a8, lda, b8, ldb), scatter, s, what);
   if (st) return st;
   const int64_t blocks = cdiv(cdiv(M, 8) * 2 * H, 4);     // one wave per 8 tokens x (kind, head)
-  C4Q_REQUIRE(blocks < (1ll << 31), C4Q_ERR_SHAPE, "%s: problem too large", what);
+  C4Q_REQUIRE(blocks < (1ll << 29), C4Q_ERR_SHAPE, "%s: problem too large", what);
   if (R % 8 == 0)
     hipLaunchKernelGGL(head_norm_rope_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, s, epi, H);
   else
