@@ -55,7 +55,13 @@ typedef __bf16   bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8  __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2  __attribute__((ext_vector_type(2)));
 
-constexpr int kGroupM = 8;           // tile rows per raster band
+// Tile rows per raster band. Measured on MI355X over band heights 1, 2, 3,
+// 4, 6 and 8 (fp8 16384x5120->13824 / 16384x13824->5120, int8 9216x5120 with
+// N 5120 / 13824 and 9216x13824->5120, the INT8 pair, W8A16 QKV / block):
+// 3 gains 5-6 % on the K = 5120 shapes over 8 and is within 1 % of the best
+// everywhere else (2 and 6 also win on the K = 5120 shapes but lose 1-4 %
+// on the K = 13824 down-projection and the INT8 pair).
+constexpr int kGroupM = 3;
 
 template <class T, class F>
 __device__ __forceinline__ T bitcast(const F& f) { return __builtin_bit_cast(T, f); }
