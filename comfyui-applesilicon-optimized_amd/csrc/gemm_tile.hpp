@@ -487,7 +487,11 @@ struct StoreMap {
 };
 
 // Store one unit (GPU packed 4-column groups) at (m, n .. n+nv-1): one 8- or
-// 16-byte store where the row allows, else per group.
+// 16-byte store where the row allows, else per group. The 16-byte stores are
+// non-temporal: the output is written once and not read back by the kernel,
+// and streaming it keeps the A/B panels in cache (MI355X, interleaved A/B:
+// fp8 16384x5120->13824 and 16384x13824->5120 +5 %, INT8 pair, W8A16 QKV and
+// the int8 WAN shapes within noise).
 template <int GPU, class Epi, class Packed>
 __device__ __forceinline__ void store_unit(const Epi& epi, int64_t m, int64_t n, int nv,
                                            const Packed* p) {
@@ -495,7 +499,9 @@ __device__ __forceinline__ void store_unit(const Epi& epi, int64_t m, int64_t n,
   if (epi.vec && nv >= 4 * GPU) {
     uint8_t* dst = epi.addr(m, n);
     if constexpr (sizeof(Packed) == 8 && GPU == 2)
-      *reinterpret_cast<uint4*>(dst) = uint4{p[0].x, p[0].y, p[1].x, p[1].y};
+      __builtin_nontemporal_store(u32x4{p[0].x, p[0].y, p[1].x, p[1].y}, reinterpret_cast<u32x4*>(dst));
+    else if constexpr (sizeof(Packed) == 16)
+      __builtin_nontemporal_store(bitcast<u32x4>(p[0]), reinterpret_cast<u32x4*>(dst));
     else
       *reinterpret_cast<Packed*>(dst) = p[0];
     return;
