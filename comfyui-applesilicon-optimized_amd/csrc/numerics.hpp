@@ -6,6 +6,8 @@
 //   * fp8 e4m3fn -> float : exact decode;
 //   * float -> fp8 e4m3fn : round to nearest even, |x| >= 480 and NaN -> NaN
 //                           (torch's cast; callers clamp to +-448 first).
+// The one hardware conversion here, e4m3_pair, is checked against f32_e4m3
+// for every float bit pattern.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -108,5 +110,34 @@ C4Q_HD uint8_t f32_e4m3(float f) {
   r += 0x7FFFFu + ((r >> 20) & 1u);
   return (uint8_t)(sign | (r >> 20));
 }
+
+// Clamp to [-448, 448] the way torch's clamp does (NaN passes through).
+C4Q_HD float clamp448(float v) { return v > 448.0f ? 448.0f : (v < -448.0f ? -448.0f : v); }
+
+// e4m3fn codes of clamp448(a) (bits 0-7) and clamp448(b) (bits 8-15):
+// f32_e4m3(clamp448(.)) of each, by the gfx950 conversion v_cvt_pk_fp8_f32
+// (OCP e4m3, round to nearest even; its inputs are within +-448 here). A NaN
+// takes the integer path (sign | 0x7F). Equal to f32_e4m3(clamp448(.)) for
+// every float bit pattern in either slot, checked on the GPU
+// (tests/test_gpu_numerics.py).
+__device__ __forceinline__ uint32_t e4m3_pair(float a, float b) {
+  if (__builtin_expect(a != a || b != b, 0))
+    return (uint32_t)f32_e4m3(clamp448(a)) | ((uint32_t)f32_e4m3(clamp448(b)) << 8);
+  const float ca = fminf(fmaxf(a, -448.0f), 448.0f), cb = fminf(fmaxf(b, -448.0f), 448.0f);
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(ca, cb, 0, false) & 0xFFFFu;
+}
+
+// The per-tensor fp8 activation quantizer divides by s = RN(amax / 448) with
+// r = RN(1 / s) and div_bf16_operands: one multiply and two fused steps per
+// element instead of an IEEE division. Used for 2^-80 <= s <= 2^126 (amax
+// from about 3.7e-22 up, finite): then every quotient of magnitude 2^-10 or
+// more (the smallest that does not encode as zero) has |x| >= 2^-90, so the
+// residual is a normal float and exact, as the residual step needs; smaller
+// quotients encode as a signed zero either way. With smaller s a subnormal x
+// can leave an inexact residual (206 of the bf16 pairs below 2^-80 differ).
+// The e4m3 code of the result equals the code of the correctly rounded
+// quotient for every bf16 (f16) x and every s this quantizer forms from a
+// bf16 (f16) amax >= |x| in that range, checked on the GPU.
+C4Q_HD bool rcp_quot_ok(float s) { return s >= 8.27180613e-25f && s <= 8.50705917e37f; }
 
 }  // namespace c4q

@@ -448,21 +448,20 @@ absmax_kernel(const uint16_t* x, int64_t n, float* amax) {
 
 // q = e4m3fn(clamp(x / scale, -448, 448)); scale = amax / 448, or 1 for an
 // all-zero tensor. NaN passes the clamp and encodes as NaN, as torch's
-// clamp-then-cast does. VEC: x 16-byte and q 8-byte aligned.
-template <bool BF16>
-__device__ __forceinline__ uint32_t quant_e4m3(uint16_t h, float s) {
-  float v = half_f32(h, BF16) / s;
-  v = v > 448.0f ? 448.0f : (v < -448.0f ? -448.0f : v);
-  return f32_e4m3(v);
+// clamp-then-cast does. VEC: x 16-byte and q 8-byte aligned. The quotient
+// comes from one reciprocal per thread and a fused residual step per element
+// where rcp_quot_ok(scale) (its e4m3 code equals that of the IEEE quotient,
+// see numerics.hpp), else from the IEEE division; the codes from e4m3_pair
+// (the hardware conversion, equal to f32_e4m3 of the clamped value).
+template <bool BF16, bool FAST>
+__device__ __forceinline__ float quot_scale(uint16_t h, float s, float r) {
+  const float x = half_f32(h, BF16);
+  return FAST ? div_bf16_operands(x, s, r) : x / s;
 }
 
-template <bool BF16, bool VEC>
-__global__ void __launch_bounds__(256)
-quant_pertensor_kernel(const uint16_t* x, int64_t n, uint8_t* q, float* scale,
-                       const float* amax) {
-  float s = amax[0] / 448.0f;
-  if (s == 0.0f) s = 1.0f;
-  if (blockIdx.x == 0 && threadIdx.x == 0) scale[0] = s;
+template <bool BF16, bool VEC, bool FAST>
+__device__ __forceinline__ void quant_pertensor_body(const uint16_t* x, int64_t n, uint8_t* q,
+                                                     float s, float r) {
   const int64_t stride = (int64_t)gridDim.x * 256;
   const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
   int64_t done = 0;
@@ -473,16 +472,30 @@ quant_pertensor_kernel(const uint16_t* x, int64_t n, uint8_t* q, float* scale,
       const uint32_t w[4] = {u.x, u.y, u.z, u.w};
       uint32_t o[2];
 #pragma unroll
-      for (int c = 0; c < 2; ++c)
-        o[c] = quant_e4m3<BF16>((uint16_t)w[2 * c], s) |
-               (quant_e4m3<BF16>((uint16_t)(w[2 * c] >> 16), s) << 8) |
-               (quant_e4m3<BF16>((uint16_t)w[2 * c + 1], s) << 16) |
-               (quant_e4m3<BF16>((uint16_t)(w[2 * c + 1] >> 16), s) << 24);
+      for (int c = 0; c < 2; ++c) {
+        const uint32_t lo = e4m3_pair(quot_scale<BF16, FAST>((uint16_t)w[2 * c], s, r),
+                                      quot_scale<BF16, FAST>((uint16_t)(w[2 * c] >> 16), s, r));
+        const uint32_t hi = e4m3_pair(quot_scale<BF16, FAST>((uint16_t)w[2 * c + 1], s, r),
+                                      quot_scale<BF16, FAST>((uint16_t)(w[2 * c + 1] >> 16), s, r));
+        o[c] = lo | (hi << 16);
+      }
       *reinterpret_cast<uint2*>(q + i * 8) = uint2{o[0], o[1]};
     }
     done = n8 * 8;
   }
-  for (int64_t i = done + t; i < n; i += stride) q[i] = (uint8_t)quant_e4m3<BF16>(x[i], s);
+  for (int64_t i = done + t; i < n; i += stride)
+    q[i] = (uint8_t)(e4m3_pair(quot_scale<BF16, FAST>(x[i], s, r), 0.0f) & 0xFFu);
+}
+
+template <bool BF16, bool VEC>
+__global__ void __launch_bounds__(256)
+quant_pertensor_kernel(const uint16_t* x, int64_t n, uint8_t* q, float* scale,
+                       const float* amax) {
+  float s = amax[0] / 448.0f;
+  if (s == 0.0f) s = 1.0f;
+  if (blockIdx.x == 0 && threadIdx.x == 0) scale[0] = s;
+  if (rcp_quot_ok(s)) quant_pertensor_body<BF16, VEC, true>(x, n, q, s, 1.0f / s);
+  else quant_pertensor_body<BF16, VEC, false>(x, n, q, s, 0.0f);
 }
 
 // fp8 -> T dequant with the same conversion routine the W8A16 GEMM uses

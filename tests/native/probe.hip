@@ -87,6 +87,64 @@ extern "C" int c4q_probe_div_bf16_exhaustive(unsigned long long* out, void* stre
   return (int)hipGetLastError();
 }
 
+// e4m3_pair against f32_e4m3(clamp448(.)) for every float bit pattern u in
+// slot 0 and u * 0x9E3779B1 (a bijection of the 2^32 patterns) in slot 1.
+__global__ void __launch_bounds__(256) e4m3_pair_all(unsigned long long* bad, uint32_t* first) {
+  const uint64_t t = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+  unsigned long long n = 0;
+  for (uint64_t k = 0; k < 256; ++k) {
+    const uint32_t u = (uint32_t)(t * 256 + k), v = u * 0x9E3779B1u;
+    const float a = bits_f32(u), b = bits_f32(v);
+    const uint32_t hw = e4m3_pair(a, b);
+    const uint32_t ref = (uint32_t)f32_e4m3(clamp448(a)) | ((uint32_t)f32_e4m3(clamp448(b)) << 8);
+    if (hw != ref) {
+      if (n == 0) atomicMin(first, u);
+      ++n;
+    }
+  }
+  if (n) atomicAdd(bad, n);
+}
+
+// The per-tensor fp8 quantizer's quotient: for every non-NaN 16-bit x and
+// every positive finite 16-bit amax with s = RN(amax / 448) on the
+// reciprocal path (rcp_quot_ok), the e4m3 code of div_bf16_operands(x, s,
+// RN(1/s)) against the code of the IEEE quotient x / s (both clamped).
+// Thread t: x = t >> 8, amax = 1 + 128 (t & 255) + k. which: 0 bf16, 1 f16.
+template <bool BF16>
+__global__ void __launch_bounds__(256) quot_e4m3_all(unsigned long long* bad, uint32_t* first) {
+  const uint32_t t = blockIdx.x * 256u + threadIdx.x;
+  const uint32_t xb = t >> 8;
+  const uint32_t inf = BF16 ? 0x7F80u : 0x7C00u;
+  if ((xb & 0x7FFFu) > inf) return;                          // NaN x
+  const float x = BF16 ? bf16_f32((uint16_t)xb) : __builtin_bit_cast(_Float16, (uint16_t)xb);
+  unsigned long long n = 0;
+  for (uint32_t k = 0; k < 128; ++k) {
+    const uint32_t ab = 1u + 128u * (t & 255u) + k;
+    if (ab >= inf) break;                                    // positive finite amax only
+    const float amax = BF16 ? bf16_f32((uint16_t)ab) : (float)__builtin_bit_cast(_Float16, (uint16_t)ab);
+    if (fabsf(x) > amax) continue;                           // |x| <= amax in any real tensor
+    const float s = amax / 448.0f;
+    if (!rcp_quot_ok(s)) continue;
+    const float fast = div_bf16_operands(x, s, 1.0f / s);
+    if ((e4m3_pair(fast, 0.0f) & 0xFFu) != f32_e4m3(clamp448(x / s))) {
+      if (n == 0) atomicMin(first, (xb << 16) | ab);
+      ++n;
+    }
+  }
+  if (n) atomicAdd(bad, n);
+}
+
+// which: 0 = e4m3_pair over all patterns, 1 = bf16 quotients, 2 = f16
+// quotients. out: device [2] u64 (mismatch count, first mismatch).
+extern "C" int c4q_probe_e4m3_exhaustive(int which, unsigned long long* out, void* stream) {
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  uint32_t* first = reinterpret_cast<uint32_t*>(out + 1);
+  if (which == 0) hipLaunchKernelGGL(e4m3_pair_all, dim3(65536), dim3(256), 0, s, out, first);
+  else if (which == 1) hipLaunchKernelGGL(quot_e4m3_all<true>, dim3(65536), dim3(256), 0, s, out, first);
+  else hipLaunchKernelGGL(quot_e4m3_all<false>, dim3(65536), dim3(256), 0, s, out, first);
+  return (int)hipGetLastError();
+}
+
 // ---------------------------------------------------------- tile plans ---
 // Host-side enumeration of the launches a GEMM's tile plan issues
 // (plan_launches, tile_at -- the functions the library runs). cover

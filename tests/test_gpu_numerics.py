@@ -21,6 +21,8 @@ def probe():
     lib.c4q_probe_cvt_exhaustive.restype = ctypes.c_int
     lib.c4q_probe_div_bf16_exhaustive.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
     lib.c4q_probe_div_bf16_exhaustive.restype = ctypes.c_int
+    lib.c4q_probe_e4m3_exhaustive.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    lib.c4q_probe_e4m3_exhaustive.restype = ctypes.c_int
     return lib
 
 
@@ -44,3 +46,20 @@ def test_reciprocal_quotient_matches_division_for_bf16_operands(dev, probe):
     assert rc == 0
     bad, first = out.cpu().tolist()
     assert bad == 0, f"{bad} pairs differ (first x<<16|s = 0x{first & 0xFFFFFFFF:08x})"
+
+
+@pytest.mark.parametrize("which,name", [(0, "e4m3 pair conversion, every float pattern"),
+                                        (1, "bf16 x, bf16 amax quotient"),
+                                        (2, "f16 x, f16 amax quotient")])
+def test_fp8_pertensor_quantizer_arithmetic(dev, probe, which, name):
+    """The per-tensor fp8 activation quantizer's arithmetic: the hardware
+    pair conversion equals the integer e4m3 rounding of the clamped value for
+    every float (NaN included, both slots), and the reciprocal quotient gives
+    the IEEE quotient's e4m3 code for every 16-bit x and every scale the
+    quantizer forms from a 16-bit amax >= |x|."""
+    out = torch.tensor([0, 0xFFFFFFFF], dtype=torch.int64, device=dev)
+    rc = probe.c4q_probe_e4m3_exhaustive(which, out.data_ptr(),
+                                         torch.cuda.current_stream(dev).cuda_stream)
+    assert rc == 0
+    bad, first = out.cpu().tolist()
+    assert bad == 0, f"{name}: {bad} mismatches (first 0x{first & 0xFFFFFFFF:08x})"
