@@ -555,6 +555,27 @@ def test_fp8_quant_pertensor_exact(dev, shape, mult):
     assert_bits_equal(u8(q), qr, "fp8 quant")
 
 
+@pytest.mark.parametrize("dtype,mult", [
+    (torch.bfloat16, 1e-24),    # scale below 2^-80: the IEEE-divide path
+    (torch.bfloat16, 3e-21),    # just above it: the reciprocal path
+    (torch.bfloat16, 1e30),     # large scale
+    (torch.bfloat16, 2e-38),    # subnormal-heavy bf16 input, IEEE path
+    (torch.float16, 1.0),
+    (torch.float16, 3e-5),      # f16 subnormals
+    (torch.float16, 1e4),       # toward the f16 maximum (no infinities)
+])
+def test_fp8_quant_pertensor_scale_ranges(dev, dtype, mult):
+    """Both quotient paths of the per-tensor fp8 quantizer (reciprocal step
+    for 2^-80 <= scale <= 2^126, IEEE divide otherwise) against the oracle,
+    bit-exact, with a ragged length for the scalar tail."""
+    g = gen(31)
+    x = (torch.randn(777, 301, generator=g) * mult).to(dtype)
+    q, s = ops.fp8_quant_pertensor(x.to(dev))
+    qr, sr = of.quant_pertensor(bits16(x), "bf16" if dtype == torch.bfloat16 else "f16")
+    assert s.item() == sr
+    assert_bits_equal(u8(q), qr, f"fp8 quant {dtype} x{mult}")
+
+
 def test_fp8_quant_zero_tensor(dev):
     x = torch.zeros(64, 64, dtype=torch.bfloat16)
     q, s = ops.fp8_quant_pertensor(x.to(dev))
