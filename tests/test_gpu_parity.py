@@ -175,7 +175,10 @@ def test_f16_outputs_round_f32_results_once(dev):
 
 # ConvRot: fused head merge + 256-wide rotation + rowwise quant
 MRQ_CASES = [(1, 24, 300, 128), (1, 12, 257, 256), (2, 3, 50, 256), (1, 8, 33, 96),
-             (1, 1, 5, 256), (1, 120, 3, 128), (1, 64, 9, 100)]   # D=100: 2-byte gathers
+             (1, 1, 5, 256), (1, 120, 3, 128), (1, 64, 9, 100),   # D=100: 2-byte gathers
+             # more rows than the persistent grid holds: each workgroup loops over
+             # rows with the next row's gather in flight
+             (1, 2, 6000, 128), (2, 12, 1100, 256)]
 
 
 def _bhsd(g, B, H, S, D):
