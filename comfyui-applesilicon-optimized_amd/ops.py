@@ -8,8 +8,11 @@ RuntimeError before any work is enqueued):
     i8_matmul2d_nt_fused_cs_half,
     i8_quant_rowwise, i8_merge_rot_quant, i8_swiglu_rot
                                      (_patches/int8_ext/int8_gemm.mm:2626-2715)
-    fp8fp8_matmul2d_nt               (_patches/fp8_ext/fp8_matmul2d.mm:229-265)
-    w8a16_f32, w8a16_bias_bf16       (_patches/fp8s_ext/w8a16_gemm.mm:286-329)
+    fp8fp8_matmul2d_nt, fp8_matmul2d_nt, fp8_matmul2d
+                                     (_patches/fp8_ext/fp8_matmul2d.mm:229-353)
+    w8a16_f32, w8a16_bias_bf16, num_variants
+                                     (_patches/fp8s_ext/w8a16_gemm.mm:286-329)
+    warmup                           (each module's pipeline warm-up)
 
 plus the whole-operation forms the patch layer uses: ``int_mm``
 (torch._int_mm), ``scaled_mm`` (torch._scaled_mm), ``fp8_quant_pertensor``,
@@ -589,41 +592,104 @@ def w8a16_bias_bf16(a, w_u8, bias=None, variant=-1):
     return w8a16_linear(a, w_u8, bias=bias, out_dtype=torch.bfloat16)
 
 
+def fp8_matmul2d_nt(a, w_u8, N=None):
+    """C[M,N] f32 = A[M,K] (f16 / bf16) @ W^T, W [N,K] e4m3fn bytes, no
+    scale (reference fp8_ext ``fp8_matmul2d_nt``,
+    ``_patches/fp8_ext/fp8_matmul2d.mm:312-353``): the W8A16 route with an
+    f32 output. The reference requires fp16 activations; bf16 is accepted
+    too."""
+    _req(a.dim() == 2, "a must be 2D")
+    w_u8 = _as_u8(w_u8)
+    _req(w_u8.dim() == 2, "w must be 2D [N,K]")
+    _req(N is None or int(N) == w_u8.size(0), "N does not match the weight")
+    return w8a16_linear(a, w_u8, out_dtype=torch.float32)
+
+
+def fp8_matmul2d(a, w_u8, N=None):
+    """C[M,N] f32 = A[M,K] (f16 / bf16) @ W, W [K,N] e4m3fn bytes (reference
+    fp8_ext ``fp8_matmul2d``, ``_patches/fp8_ext/fp8_matmul2d.mm:268-310``).
+    The [K,N] weight is transposed to the [N,K] operand order once per call
+    (one device copy of the fp8 bytes), then the W8A16 route runs."""
+    _req(a.dim() == 2, "a must be 2D")
+    w_u8 = _as_u8(w_u8)
+    _req(w_u8.dim() == 2 and w_u8.size(0) == a.size(1), "w must be [K,N] with K = a.size(1)")
+    _req(N is None or int(N) == w_u8.size(1), "N does not match the weight")
+    return w8a16_linear(a, w_u8.t().contiguous(), out_dtype=torch.float32)
+
+
 # ------------------------------------------------------ activation tables ---
 
 _TABLES = {}
 
 
-def act_table(name, device):
-    """65,536-entry bf16 table of activation `name` ('silu' | 'gelu_tanh')
-    built once per device with torch's own op on that device, so a fused
-    epilogue reproduces the unfused "bf16 tensor -> F.<act>" chain there."""
+def _all_bf16_cpu():
+    return torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+
+
+def _table_on(key, device, build):
+    """Table(s) `build()` made once on the CPU, copied once per device."""
     device = torch.device(device)
-    key = (name, device)
-    t = _TABLES.get(key)
+    t = _TABLES.get((key, device))
     if t is None:
-        v = torch.arange(65536, dtype=torch.int32, device=device).to(torch.int16).view(torch.bfloat16)
+        cpu = _TABLES.get((key, None))
+        if cpu is None:
+            cpu = build()
+            _TABLES[(key, None)] = cpu
+        if isinstance(cpu, tuple):
+            t = tuple(c.to(device) for c in cpu)
+        else:
+            t = cpu.to(device)
+        _TABLES[(key, device)] = t
+    return t
+
+
+def act_table(name, device):
+    """65,536-entry bf16 table of activation `name` ('silu' | 'gelu_tanh'):
+    torch's CPU op over every bf16 value -- the unfused "bf16 tensor ->
+    F.<act>" chain the fused epilogues reproduce -- built once and copied to
+    `device`. (torch's ROCm kernels for these ops round a few entries
+    differently from its CPU kernels; the CPU tables are the ones the
+    reference's eager chain is pinned to.)"""
+    def build():
+        v = _all_bf16_cpu()
         if name == "silu":
             r = F.silu(v)
         elif name == "gelu_tanh":
             r = F.gelu(v, approximate="tanh")
         else:
             raise C4QError(f"unknown activation {name!r}")
-        t = r.contiguous().view(torch.int16)
-        _TABLES[key] = t
-    return t
+        return r.contiguous().view(torch.int16)
+    if name not in ("silu", "gelu_tanh"):
+        raise C4QError(f"unknown activation {name!r}")
+    return _table_on(name, device, build)
 
 
 def situ_tables(device):
     """MOSS SiTU tables T_h = 25 tanh(v/25), T_g = 4 tanh(v/4) sigmoid(v) over
-    every bf16 v, each op in bf16 (reference _patches/moss_fast.py:97-99)."""
-    device = torch.device(device)
-    key = ("situ", device)
-    t = _TABLES.get(key)
-    if t is None:
-        v = torch.arange(65536, dtype=torch.int32, device=device).to(torch.int16).view(torch.bfloat16)
+    every bf16 v, each op in bf16 (reference _patches/moss_fast.py:97-99),
+    built with torch's CPU ops and copied to `device`."""
+    def build():
+        v = _all_bf16_cpu()
         th = (25.0 * torch.tanh(v / 25.0)).contiguous().view(torch.int16)
         tg = (4.0 * torch.tanh(v / 4.0) * torch.sigmoid(v)).contiguous().view(torch.int16)
-        t = (th, tg)
-        _TABLES[key] = t
-    return t
+        return (th, tg)
+    return _table_on("situ", device, build)
+
+
+# ------------------------------------------------ module-level utilities ---
+
+def warmup():
+    """The reference modules' ``warmup()`` builds their Metal pipelines
+    (``_patches/int8_ext/int8_gemm.mm:2691``, ``_patches/fp8_ext/fp8_matmul2d.mm:359``,
+    ``_patches/fp8s_ext/w8a16_gemm.mm:325``). Here it loads libcdna4q.so
+    (kernels are compiled ahead of time) and returns True."""
+    _lib.load()
+    return True
+
+
+def num_variants():
+    """Count of the reference's W8A16 Metal tile variants
+    (``_patches/fp8s_ext/w8a16_gemm.mm:162-169,324``); the ``variant``
+    argument of ``w8a16_f32`` / ``w8a16_bias_bf16`` is accepted and ignored
+    here (tiles are planned by shape)."""
+    return 4

@@ -11,19 +11,22 @@ Mirrors ``_patches/int8_linear_kernel_mps.py`` (and the int8-fast seam of
 * ``_int8_linear_prequant`` dispatches by scale layout (``:152-215``): a
   per-tensor scale with bf16 output uses the fused per-row epilogue
   (``row_scale = weight_scale * x_scale``), a per-channel scale the fused
-  per-channel epilogue, anything else the raw int32 GEMM followed by the
-  reference's eager rescale (chunked ``C.float() * (w_scale * x_scale)``,
+  per-channel epilogue (bf16, or fp16 through the half epilogue of
+  ``wan_fp16.maybe_prequant``), anything else the raw int32 GEMM followed by
+  the reference's eager rescale (chunked ``C.float() * (w_scale * x_scale)``,
   ``.to(out_dtype)``, ``+ bias``) on the GPU;
 * ``_quant_cached`` keeps a 1-slot cache of the quantized activation keyed
   by a weak reference to the input tensor (``:97-140``), so the q/k/v (and
   gate/up) projections of a block quantize their shared input once;
 * ``_try_int8_kernel_forward`` is the Linear.forward eligibility gate
   (``:779-830``) and ``install`` wraps comfy's ``mixed_precision_ops``
-  factory (``:862-894``) when ComfyUI is importable;
-* ``int8_forward_dynamic[_per_row]`` replace int8-fast's wide-batch forwards
-  (``int8_linear_mps.py:54-63``) with the same W8A8 computation (the
-  reference re-routes them to a bf16 dequant + F.linear on MPS; on MI355X
-  the int8 kernel is the fast path).
+  factory (``:862-894``, with its ``disabled`` filter) and its
+  ``linear_input_act`` helper (``:897-977``) when ComfyUI is importable;
+* ``int8_forward_dynamic[_per_row]`` are the W8A8 computation that
+  ``patches/int8_fast.py`` installs in place of int8-fast's wide-batch
+  forwards (``int8_linear_mps.py:54-63``; the reference re-routes them to a
+  bf16 dequant + F.linear on MPS, on MI355X the int8 kernel is the fast
+  path).
 
 * ``int8_o_proj_prequant`` is the fused o-projection from the attention
   layout (``:436-535``): head merge + ConvRot + rowwise quant in one kernel
@@ -47,6 +50,7 @@ summation order; comfy_kitchen is not available, so that equivalence is
 unpinned). Not supported here (those calls keep the original function):
 other ConvRot inputs, non-int8 weights, tensors off the ROCm device.
 """
+import inspect
 import os
 import weakref
 
@@ -62,6 +66,7 @@ _installed = False
 _orig_int8_linear = None
 _act_cache = None      # (x_weakref, convrot, groupsize, x_8, x_scale)
 _RESCALE_CHUNK_BYTES = 256 * 1024 * 1024
+_RUNTIME_LORA_ATTR = "_asfp8_runtime_lora"   # attribute a runtime LoRA adapter sets
 
 
 def _convrot_ok(x, convrot_groupsize):
@@ -114,6 +119,14 @@ def _int8_linear_prequant(x_8, x_scale, weight, weight_scale, bias, out_dtype, i
     weight_scale = weight_scale.reshape(-1)
     n = weight.shape[0]
     out_shape = (*input_shape[:-1], n)
+    if out_dtype == torch.float16 and weight_scale.numel() == n:
+        # fp16 output, per-channel scale: the fused half epilogue rounds
+        # f32(C) * (w_scale[n] * x_scale[m]) to fp16 and adds the fp16 bias
+        # with a second rounding -- the eager chain below, byte for byte
+        # (reference ``wan_fp16.maybe_prequant``, ``_patches/wan_fp16.py:17-48``)
+        return ops.i8_matmul2d_nt_fused_cs_half(
+            x_8, weight, x_scale.reshape(-1).float().contiguous(),
+            weight_scale.float().contiguous(), bias).reshape(out_shape)
     if out_dtype == torch.bfloat16 and weight_scale.numel() == 1:
         row_scale = (weight_scale.float() * x_scale.reshape(-1).float()).contiguous()
         bias_arg = bias.to(torch.bfloat16) if bias is not None else None
@@ -163,7 +176,7 @@ def _try_int8_kernel_forward(self, input):
     ROCm device, the weight a TensorWiseINT8Layout QuantizedTensor without
     transposition (with ConvRot: an input the rotation pass takes), and the
     layer has no full-precision flag, force-cast or LoRA weight/bias
-    functions."""
+    functions. A call the kernels reject (C4QError) also returns None."""
     if not _common.on_device(input) or _common.is_quantized_int8(input):
         return None
     w = getattr(self, "weight", None)
@@ -182,7 +195,13 @@ def _try_int8_kernel_forward(self, input):
     gs = getattr(params, "convrot_groupsize", 256)
     if convrot and not _convrot_ok(input, gs):
         return None
-    return _int8_linear_kernel(input, w._qdata, params.scale, self.bias, input.dtype, convrot, gs)
+    try:
+        return _int8_linear_kernel(input, w._qdata, params.scale, self.bias, input.dtype,
+                                   convrot, gs)
+    except C4QError as e:
+        # a call the kernels reject keeps comfy's forward (reference :816-830)
+        print(f"{TAG} kernel forward fell back ({e})")
+        return None
 
 
 def _plain_int8_layer(layer):
@@ -213,7 +232,7 @@ def _int8_qkv_prequant(layer, x, heads, head_dim, norm_rope):
 
     if not _on("INT8_QKV_SCATTER") or (norm_rope is not None and not _on("INT8_QKV_NORM_ROPE")):
         return None
-    if getattr(layer, "_asfp8_runtime_lora", None) is not None:
+    if getattr(layer, _RUNTIME_LORA_ATTR, None) is not None:
         return None
     if (not isinstance(x, torch.Tensor) or x.dim() != 2 or not _common.on_device(x)
             or x.dtype != torch.bfloat16 or not x.is_contiguous()):
@@ -305,7 +324,7 @@ def int8_mlp_bridge(fc1, fc2, x):
             or os.environ.get("ASFP8_INT8_SWIGLU", "1") != "1"
             or os.environ.get("ASFP8_INT8_SWIGLU_ROT", "1") != "1"):
         return None
-    if any(getattr(layer, "_asfp8_runtime_lora", None) is not None for layer in (fc1, fc2)):
+    if any(getattr(layer, _RUNTIME_LORA_ATTR, None) is not None for layer in (fc1, fc2)):
         return None
     if (not isinstance(x, torch.Tensor) or x.dim() != 2 or not _common.on_device(x)
             or x.dtype != torch.bfloat16 or not x.is_contiguous()):
@@ -344,8 +363,13 @@ def _try_int8_swiglu_forward(linear, x):
     """``linear(swiglu(x))`` (reference ``:708-775``), or None to fall back.
     With a ConvRot weight (group size 256) and a contiguous bf16 input: the
     fused SwiGLU + rotation pass, rowwise quant, the INT8 GEMM; without
-    ConvRot: the bf16 SwiGLU (torch ops) and the ordinary kernel path."""
+    ConvRot: the bf16 SwiGLU (torch ops) and the ordinary kernel path.
+    Layers with a runtime LoRA adapter are not served (the caller's
+    ``linear(swiglu(x))`` keeps the adapter); a call the kernels reject
+    falls back too."""
     if not _common.on_device(x) or _common.is_quantized_int8(x):
+        return None
+    if getattr(linear, _RUNTIME_LORA_ATTR, None) is not None:
         return None
     w = _plain_int8_layer(linear)
     if w is None:
@@ -355,18 +379,23 @@ def _try_int8_swiglu_forward(linear, x):
         return None
     half = wide // 2
     params = w._params
-    if getattr(params, "convrot", False):
-        x2 = x.reshape(-1, wide)
-        if (getattr(params, "convrot_groupsize", 256) != 256 or x.dtype != torch.bfloat16
-                or not x2.is_contiguous() or half % 256
-                or os.environ.get("C4Q_INT8_SWIGLU_ROT", "1") == "0"):
-            return None
-        rot = ops.i8_swiglu_rot(x2)
-        x_8, x_scale = ops.i8_quant_rowwise(rot)
-        return _int8_linear_prequant(x_8, x_scale, w._qdata, params.scale, linear.bias, x.dtype,
-                                     (*x.shape[:-1], half), split_tail=True)
-    act = torch.nn.functional.silu(x[..., :half]) * x[..., half:]
-    return _int8_linear_kernel(act, w._qdata, params.scale, linear.bias, x.dtype)
+    try:
+        if getattr(params, "convrot", False):
+            x2 = x.reshape(-1, wide)
+            if (getattr(params, "convrot_groupsize", 256) != 256 or x.dtype != torch.bfloat16
+                    or not x2.is_contiguous() or half % 256
+                    or os.environ.get("C4Q_INT8_SWIGLU_ROT",
+                                      os.environ.get("ASFP8_INT8_SWIGLU_ROT", "1")) == "0"):
+                return None
+            rot = ops.i8_swiglu_rot(x2)
+            x_8, x_scale = ops.i8_quant_rowwise(rot)
+            return _int8_linear_prequant(x_8, x_scale, w._qdata, params.scale, linear.bias,
+                                         x.dtype, (*x.shape[:-1], half), split_tail=True)
+        return _int8_linear_kernel(_swiglu_activation(x), w._qdata, params.scale, linear.bias,
+                                   x.dtype)
+    except C4QError as e:
+        print(f"{TAG} SwiGLU forward fell back ({e})")
+        return None
 
 
 # ---------------------------------------------------------- int8-fast seam ---
@@ -389,30 +418,66 @@ def int8_forward_dynamic_per_row(x, weight, weight_scale, bias, compute_dtype):
     return _w8a8_dynamic(x, weight, weight_scale, bias, compute_dtype)
 
 
-def install():
-    """Wrap comfy's ``mixed_precision_ops`` factory so generated int8 Linear
-    layers route through the kernel (reference ``:837-894``). Returns True
-    when installed (ComfyUI importable and a ROCm device present)."""
-    global _installed, _orig_int8_linear
-    if _installed:
-        return True
-    if not _common.rocm_available():
-        return False
+def _swiglu_activation(x):
+    """H3's bf16 SwiGLU, ``silu(x[..., :F]) * x[..., F:]`` in torch ops
+    (reference ``_swiglu_activation`` ``:693-705`` without its Metal helper,
+    which computes the same bytes)."""
+    half = x.shape[-1] // 2
+    return torch.nn.functional.silu(x[..., :half]) * x[..., half:]
+
+
+def _linear_input_act_wrapper(orig_lia):
+    """``comfy.ops.linear_input_act(linear, x, input_act)`` with the SwiGLU
+    down-projection on the INT8 route (reference ``:897-977``). comfy calls
+    this helper for SwiGLU'd down-projections instead of ``Linear.forward``,
+    so the factory wrap alone never sees them. Extended calls (extra
+    positional or keyword arguments) keep the original helper; a plain
+    ``input_act is None`` call on a module runs the module (and with it the
+    patched Linear forward); a SwiGLU call the kernel route declines on a
+    layer with a runtime LoRA adapter runs ``linear(swiglu(x))`` so the
+    adapter hook still fires. Switches: ``C4Q_INT8_SWIGLU`` /
+    ``ASFP8_INT8_SWIGLU`` and ``ASFP8_INT8_PLAIN_LIA`` (=0 off)."""
+    def linear_input_act(linear, x, input_act, *args, **kwargs):
+        if args or kwargs:
+            return orig_lia(linear, x, input_act, *args, **kwargs)
+        if input_act == "swiglu" and _common.env_on(
+                "C4Q_INT8_SWIGLU", os.environ.get("ASFP8_INT8_SWIGLU", "1")):
+            res = _try_int8_swiglu_forward(linear, x)
+            if res is not None:
+                return res
+        if (input_act is None and isinstance(linear, torch.nn.Module)
+                and os.environ.get("ASFP8_INT8_PLAIN_LIA", "1") == "1"):
+            return linear(x)
+        if input_act == "swiglu" and getattr(linear, _RUNTIME_LORA_ATTR, None) is not None:
+            return linear(_swiglu_activation(x))
+        return orig_lia(linear, x, input_act)
+
+    linear_input_act._c4q_wrapped = True
+    return linear_input_act
+
+
+def _wrap_factory(factory):
+    """``mixed_precision_ops`` wrapper (reference ``:862-894``): drops
+    ``"int8_tensorwise"`` from the ``disabled`` formats (ComfyUI's hardware
+    probe does not know this int8 implementation; every other exclusion is
+    kept) and patches the generated ``Linear.forward`` to try the kernel
+    route first."""
     try:
-        import comfy.ops as comfy_ops
-    except Exception:
-        return False
-    try:
-        from comfy_kitchen.backends.eager.quantization import int8_linear as orig
-        _orig_int8_linear = orig
-    except Exception:
-        _orig_int8_linear = None
-    factory = comfy_ops.mixed_precision_ops
-    if getattr(factory, "_c4q_wrapped", False):
-        _installed = True
-        return True
+        sig = inspect.signature(factory)
+    except (TypeError, ValueError):
+        sig = None
 
     def wrapped_factory(*a, **k):
+        if sig is not None:
+            try:
+                bound = sig.bind(*a, **k)
+            except TypeError:
+                bound = None
+            if bound is not None:
+                disabled = bound.arguments.get("disabled")
+                if disabled is not None:
+                    bound.arguments["disabled"] = [f for f in disabled if f != "int8_tensorwise"]
+                a, k = bound.args, bound.kwargs
         cls = factory(*a, **k)
         linear_cls = getattr(cls, "Linear", None)
         if linear_cls is not None and not getattr(linear_cls, "_c4q_int8_patched", False):
@@ -429,7 +494,40 @@ def install():
         return cls
 
     wrapped_factory._c4q_wrapped = True
-    comfy_ops.mixed_precision_ops = wrapped_factory
+    return wrapped_factory
+
+
+def _patch_comfy_ops(comfy_ops):
+    """Install the factory and ``linear_input_act`` wraps on a ``comfy.ops``
+    module (idempotent)."""
+    if not getattr(comfy_ops.mixed_precision_ops, "_c4q_wrapped", False):
+        comfy_ops.mixed_precision_ops = _wrap_factory(comfy_ops.mixed_precision_ops)
+    lia = getattr(comfy_ops, "linear_input_act", None)
+    if lia is not None and not getattr(lia, "_c4q_wrapped", False):
+        comfy_ops.linear_input_act = _linear_input_act_wrapper(lia)
+
+
+def install():
+    """Wrap comfy's ``mixed_precision_ops`` factory and ``linear_input_act``
+    helper so int8 Linear layers and SwiGLU down-projections route through
+    the kernels (reference ``:833-983``). Returns True when installed
+    (ComfyUI importable and a ROCm device present)."""
+    global _installed, _orig_int8_linear
+    if _installed:
+        return True
+    if not _common.rocm_available():
+        return False
+    try:
+        import comfy.ops as comfy_ops
+    except Exception:
+        return False
+    try:
+        from comfy_kitchen.backends.eager.quantization import int8_linear as orig
+        _orig_int8_linear = orig
+    except Exception:
+        _orig_int8_linear = None
+    _patch_comfy_ops(comfy_ops)
     _installed = True
-    print(f"{TAG} comfy int8 Linear layers routed to the int8 MFMA kernels.")
+    print(f"{TAG} comfy int8 Linear layers and SwiGLU down-projections routed to the int8 "
+          "MFMA kernels.")
     return True

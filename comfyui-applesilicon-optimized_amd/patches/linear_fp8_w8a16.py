@@ -51,12 +51,18 @@ def _weight_scale(module):
 
 
 def _eligible(module, input):
-    """Cheap per-call predicate, no device work (reference ``:89-117``)."""
+    """Per-call gate over attributes only, nothing enqueued (reference
+    ``:89-117``). Served: a plain 2-D contiguous e4m3fn weight on the ROCm
+    device (tensor subclasses such as QuantizedTensor hide their dtype or
+    keep their own forward), a bf16 / f16 input of matching K, no weight or
+    bias functions (a LoRA patch needs the decoded weight), no offload
+    bookkeeping, at most a per-tensor weight scale, and the optional size
+    gates."""
     w = getattr(module, "weight", None)
     if w is None or getattr(w, "dtype", None) != torch.float8_e4m3fn:
-        return False           # covers QuantizedTensor (dtype hidden), e5m2, non-fp8
+        return False
     if type(w) not in (torch.Tensor, torch.nn.Parameter):
-        return False           # tensor subclasses keep their own path
+        return False
     if w.dim() != 2 or not _common.on_device(w) or not w.is_contiguous():
         return False
     if input.dtype not in _ELIGIBLE_INPUT_DTYPES or not _common.on_device(input):
@@ -64,11 +70,11 @@ def _eligible(module, input):
     if input.shape[-1] != w.shape[1]:
         return False
     if len(getattr(module, "weight_function", [])) > 0 or len(getattr(module, "bias_function", [])) > 0:
-        return False           # LoRA & co. need the decoded weight
+        return False
     if hasattr(module, "_v") or hasattr(module, "_prefetch"):
-        return False           # offloaded / prefetched weights
+        return False
     if _weight_scale(module) is False:
-        return False           # only per-tensor weight scales
+        return False
     N, K = int(w.shape[0]), int(w.shape[1])
     M = input.numel() // input.shape[-1]
     if max(N, K) < _int_env("C4Q_W8A16_MIN_DIM", 0):

@@ -11,8 +11,10 @@ Everything else keeps the stock op.
 
 Differences from the reference, by design: per-row ``scale_a`` [M, 1] and
 per-column ``scale_b`` [1, N] vectors are accepted (applied in the same
-order); no size gate unless ``C4Q_FP8_MIN_DIM`` sets one; a failed self-check
-or kernel error raises instead of falling back to a decode path.
+order); no size gate unless ``C4Q_FP8_MIN_DIM`` sets one; a failed one-time
+self-check raises (a broken kernel must not go unnoticed). Calls outside the
+kernel's argument set (``out_dtype=None`` or fp8, blockwise / MX scales,
+other bias shapes) and calls the kernel rejects keep the stock ROCm op.
 """
 import os
 
@@ -36,15 +38,47 @@ def _min_dim():
         return 0
 
 
-def _fast_eligible(input, other):
-    """Pure shape / dtype predicate (reference ``:66-81``)."""
+_OUT_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
+
+
+def _scale_ok(s, n, layout_shapes, device):
+    """None, or an f32 tensor on `device` holding one value (per tensor) or
+    one per row / column in one of `layout_shapes`."""
+    if s is None:
+        return True
+    if not isinstance(s, torch.Tensor) or s.dtype != torch.float32 or s.device != device:
+        return False
+    return s.numel() == 1 or (s.numel() == n and tuple(s.shape) in layout_shapes)
+
+
+def _fast_eligible(input, other, out_dtype=torch.bfloat16, scale_a=None, scale_b=None,
+                   scale_result=None, bias=None):
+    """Pure argument predicate, no device work (reference ``:66-81``),
+    widened to every argument the fp8 kernel's epilogue takes: e4m3fn 2-D
+    operands on the ROCm device, ``out_dtype`` bf16 / f16 / f32 (None keeps
+    the stock op, whose output is then fp8), f32 scales per tensor, per row
+    ([M, 1] or [M]) for ``scale_a`` and per column ([1, N] or [N]) for
+    ``scale_b``, a per-tensor ``scale_result``, and a bf16 / f16 / f32 bias
+    of N values. Blockwise or MX (e8m0) scales and fp8 outputs keep the
+    stock op."""
     if input.dtype != torch.float8_e4m3fn or other.dtype != torch.float8_e4m3fn:
         return False
-    if not _common.on_device(input, other):
+    if not _common.on_device(input, other) or input.device != other.device:
         return False
     if input.dim() != 2 or other.dim() != 2 or input.shape[1] != other.shape[0]:
         return False
-    return max(int(other.shape[1]), int(input.shape[1])) >= _min_dim()
+    if out_dtype not in _OUT_DTYPES:
+        return False
+    M, N = int(input.shape[0]), int(other.shape[1])
+    dev = input.device
+    if not (_scale_ok(scale_a, M, ((M, 1), (M,)), dev) and _scale_ok(scale_b, N, ((1, N), (N,)), dev)
+            and _scale_ok(scale_result, 1, (), dev)):
+        return False
+    if bias is not None and not (isinstance(bias, torch.Tensor) and bias.dtype in _OUT_DTYPES
+                                 and bias.device == dev and bias.numel() == N
+                                 and bias.dim() == 1):
+        return False
+    return max(N, int(input.shape[1])) >= _min_dim()
 
 
 def _get_backend(device):
@@ -75,9 +109,14 @@ def _fast_route(input, other, scale_a, scale_b, scale_result, bias, out_dtype):
 def _rocm_scaled_mm(input, other, *, out_dtype=None, scale_a=None, scale_b=None, bias=None,
                     scale_result=None, use_fast_accum=False):
     """Replacement for ``torch._scaled_mm`` (reference ``_mps_scaled_mm``
-    ``:149-207``)."""
-    if _fast_eligible(input, other):
-        return _fast_route(input, other, scale_a, scale_b, scale_result, bias, out_dtype)
+    ``:149-207``): eligible calls take the fp8 MFMA route; a call the kernel
+    rejects falls back to the stock op, as the reference's fast route falls
+    back to its decode path (``:172-176``)."""
+    if _fast_eligible(input, other, out_dtype, scale_a, scale_b, scale_result, bias):
+        try:
+            return _fast_route(input, other, scale_a, scale_b, scale_result, bias, out_dtype)
+        except C4QError as e:
+            print(f"{TAG} fp8 route declined ({e}); using the stock op.")
     return _original(input, other, out_dtype=out_dtype, scale_a=scale_a, scale_b=scale_b,
                      bias=bias, scale_result=scale_result, use_fast_accum=use_fast_accum)
 

@@ -1,6 +1,7 @@
 """On-disk quantized linear formats, CPU only: the comfy_quant metadata
-repair (the reference's tests/test_quant_meta_fix.py cases, restated against
-this build's ``formats.fix_quant_meta`` and ``patches.quant_meta_fix``),
+repair (``formats.fix_quant_meta`` through ``patches.quant_meta_fix``, as one
+table of descriptor / weight dtype / scale cases covering the behaviour of
+reference _patches/quant_meta_fix.py:34-59),
 format detection, and loading layers from a .safetensors file into
 QuantLinear modules. The loaded layers' numerics run on the GPU in
 tests/test_gpu_formats.py."""
@@ -17,48 +18,58 @@ from cdna4q._lib import C4QError
 from cdna4q.patches import quant_meta_fix
 
 
-def _blob(conf):
-    return torch.frombuffer(bytearray(json.dumps(conf).encode()), dtype=torch.uint8)
+def _json_u8(desc):
+    return torch.tensor(list(json.dumps(desc).encode()), dtype=torch.uint8)
 
 
-def _conf(state_dict, prefix="layer."):
-    return json.loads(bytes(state_dict[f"{prefix}comfy_quant"].numpy().tobytes()))
+def _state(desc, weight_dtype, scale_shape, prefix="blk.0.mlp."):
+    """One layer's checkpoint entries: the comfy_quant descriptor as JSON
+    bytes, a 6x8 weight of `weight_dtype` and (unless `scale_shape` is None)
+    an f32 weight_scale of that shape."""
+    sd = {prefix + "comfy_quant": _json_u8(desc),
+          prefix + "weight": torch.zeros(6, 8, dtype=weight_dtype)}
+    if scale_shape is not None:
+        sd[prefix + "weight_scale"] = torch.full(scale_shape, 0.5)
+    return sd
 
 
-# -- the reference's quant_meta_fix cases ---------------------------------
-
-def test_injects_format_for_int8_with_scale():
-    sd = {"layer.comfy_quant": _blob({"convrot": True, "convrot_groupsize": 256, "per_row": True}),
-          "layer.weight": torch.zeros(4, 4, dtype=torch.int8),
-          "layer.weight_scale": torch.ones(4, 1)}
-    quant_meta_fix._maybe_fix(sd, "layer.")
-    conf = _conf(sd)
-    assert conf["format"] == "int8_tensorwise"
-    assert conf["convrot"] is True and conf["per_row"] is True        # rest preserved
+def _desc(sd, prefix="blk.0.mlp."):
+    return json.loads(sd[prefix + "comfy_quant"].numpy().tobytes().decode())
 
 
-def test_existing_format_untouched():
-    sd = {"layer.comfy_quant": _blob({"format": "int8_tensorwise", "convrot": True}),
-          "layer.weight": torch.zeros(4, 4, dtype=torch.int8),
-          "layer.weight_scale": torch.ones(4, 1)}
-    before = bytes(sd["layer.comfy_quant"].numpy().tobytes())
-    quant_meta_fix._maybe_fix(sd, "layer.")
-    assert bytes(sd["layer.comfy_quant"].numpy().tobytes()) == before
+_ROT = {"convrot": True, "convrot_groupsize": 256, "per_row": True}
+
+# (descriptor on disk, weight dtype, weight_scale shape or None) -> descriptor
+# after the repair: only an int8 weight with a scale and no declared format
+# gains "format": "int8_tensorwise"; every other key is kept as written.
+META_CASES = [
+    (_ROT, torch.int8, (6, 1), dict(_ROT, format="int8_tensorwise")),
+    ({"per_row": False}, torch.int8, (1,), {"per_row": False, "format": "int8_tensorwise"}),
+    ({}, torch.int8, (6,), {"format": "int8_tensorwise"}),
+    (dict(_ROT, format="int8_tensorwise"), torch.int8, (6, 1), dict(_ROT, format="int8_tensorwise")),
+    ({"format": "float8_e4m3fn"}, torch.int8, (6, 1), {"format": "float8_e4m3fn"}),
+    (_ROT, torch.uint8, (6, 1), _ROT),                     # packed 4-bit payload
+    (_ROT, torch.float8_e4m3fn, (6, 1), _ROT),
+    (_ROT, torch.int8, None, _ROT),                        # no weight_scale
+]
 
 
-def test_non_int8_left_alone():
-    sd = {"layer.comfy_quant": _blob({"convrot": True}),
-          "layer.weight": torch.zeros(4, 4, dtype=torch.uint8),        # packed w4, not int8
-          "layer.weight_scale": torch.ones(4, 1)}
-    quant_meta_fix._maybe_fix(sd, "layer.")
-    assert "format" not in _conf(sd)
+@pytest.mark.parametrize("desc,wdt,scale_shape,want", META_CASES)
+def test_quant_meta_repair_table(desc, wdt, scale_shape, want):
+    sd = _state(desc, wdt, scale_shape)
+    raw = sd["blk.0.mlp.comfy_quant"]
+    quant_meta_fix._maybe_fix(sd, "blk.0.mlp.")
+    assert _desc(sd) == want
+    if want == desc:                                       # untouched: same tensor object
+        assert sd["blk.0.mlp.comfy_quant"] is raw
+    assert {k for k in sd} >= {"blk.0.mlp.weight"}         # tensors themselves untouched
 
 
-def test_missing_scale_left_alone():
-    sd = {"layer.comfy_quant": _blob({"convrot": True}),
-          "layer.weight": torch.zeros(4, 4, dtype=torch.int8)}
-    quant_meta_fix._maybe_fix(sd, "layer.")
-    assert "format" not in _conf(sd)
+def test_quant_meta_repair_only_touches_its_prefix():
+    sd = _state(_ROT, torch.int8, (6, 1), "a.")
+    sd.update(_state(_ROT, torch.int8, (6, 1), "b."))
+    quant_meta_fix._maybe_fix(sd, "b.")
+    assert "format" not in _desc(sd, "a.") and _desc(sd, "b.")["format"] == "int8_tensorwise"
 
 
 def test_unparseable_descriptor_left_alone():
@@ -78,12 +89,12 @@ def test_install_wraps_comfy_loader(monkeypatch):
     seen = []
     comfy = types.ModuleType("comfy")
     comfy_ops = types.ModuleType("comfy.ops")
-    comfy_ops._load_quantized_module = lambda module, load_fn, sd, prefix: seen.append(_conf(sd, prefix))
+    comfy_ops._load_quantized_module = lambda module, load_fn, sd, prefix: seen.append(_desc(sd, prefix))
     comfy.ops = comfy_ops
     monkeypatch.setitem(sys.modules, "comfy", comfy)
     monkeypatch.setitem(sys.modules, "comfy.ops", comfy_ops)
     assert quant_meta_fix.install() is True
-    sd = {"blk.comfy_quant": _blob({"convrot": True}), "blk.weight": torch.zeros(2, 2, dtype=torch.int8),
+    sd = {"blk.comfy_quant": _json_u8({"convrot": True}), "blk.weight": torch.zeros(2, 2, dtype=torch.int8),
           "blk.weight_scale": torch.ones(2, 1)}
     comfy_ops._load_quantized_module(None, None, sd, "blk.")
     assert seen == [{"convrot": True, "format": "int8_tensorwise"}]
@@ -99,18 +110,18 @@ def _checkpoint():
     f8 = (0.02 * torch.randn(N, K, generator=g) * 400).clamp(-448, 448).to(torch.float8_e4m3fn)
     return {
         "a.weight": i8, "a.weight_scale": torch.rand(N, 1, generator=g),
-        "a.comfy_quant": _blob({"format": "int8_tensorwise"}),
+        "a.comfy_quant": _json_u8({"format": "int8_tensorwise"}),
         "a.bias": torch.randn(N, generator=g).to(torch.bfloat16),
         "b.weight": i8.clone(), "b.weight_scale": torch.rand(N, 1, generator=g),
-        "b.comfy_quant": _blob({"convrot": True, "convrot_groupsize": 256, "per_row": True}),
+        "b.comfy_quant": _json_u8({"convrot": True, "convrot_groupsize": 256, "per_row": True}),
         "c.weight": i8.clone(), "c.weight_scale": torch.tensor(0.01),
-        "c.comfy_quant": _blob({"format": "int8_tensorwise"}),
+        "c.comfy_quant": _json_u8({"format": "int8_tensorwise"}),
         "d.weight": f8, "d.scale_weight": torch.tensor(0.002),              # scaled fp8
         "e.weight": f8.clone(), "e.weight_scale": torch.tensor(0.003),
-        "e.comfy_quant": _blob({"format": "float8_e4m3fn"}),
+        "e.comfy_quant": _json_u8({"format": "float8_e4m3fn"}),
         "norm.weight": torch.ones(K, dtype=torch.bfloat16),                 # not a quantized linear
         "f.weight": torch.zeros(N, K, dtype=torch.uint8),
-        "f.comfy_quant": _blob({"format": "w4_packed"}),
+        "f.comfy_quant": _json_u8({"format": "w4_packed"}),
         "scaled_fp8": torch.zeros(0, dtype=torch.float8_e4m3fn),
     }
 
@@ -118,7 +129,7 @@ def _checkpoint():
 def test_layer_formats():
     sd = _checkpoint()
     assert formats.quantized_prefixes(sd) == ["a.", "b.", "c.", "d.", "e."]
-    assert _conf(sd, "b.")["format"] == "int8_tensorwise"                 # repaired in place
+    assert _desc(sd, "b.")["format"] == "int8_tensorwise"                 # repaired in place
     assert formats.layer_format(sd, "norm.") is None
     assert formats.layer_format(sd, "f.") is None
     with pytest.raises(C4QError):
