@@ -11,8 +11,12 @@ oracle against them:
   scaled_mm.npz       torch._scaled_mm (CPU, per-tensor scales) on a seeded case
   digests.json        sha256 of large results: the C1 config's
                       torch._int_mm INT32 output and its eager bf16 epilogue
-                      (seed 1, BASELINE C1), and the bf16 activation tables
-                      (F.silu, F.gelu tanh, the MOSS SiTU pair)
+                      (seed 1, BASELINE C1), the bf16 activation tables
+                      (F.silu, F.gelu tanh, the MOSS SiTU pair), and the C4
+                      config's rowwise-quantized activation, its scales and
+                      the unfused gate/up chain's bf16 output (seed 4,
+                      BASELINE C4: two torch._int_mm GEMMs with the eager
+                      per-channel epilogue, F.silu, then the bf16 product)
 
 Run from the repository root:  python tests/golden/make_golden.py
 """
@@ -110,7 +114,40 @@ def digests():
         "situ_g_sha256": sha(bits(4.0 * torch.tanh(v / 4.0) * torch.sigmoid(v))),
         "torch": torch.__version__,
     }
+    out.update(c4_digests())
     (OUT / "digests.json").write_text(json.dumps(out, indent=1) + "\n")
+
+
+def c4_inputs():
+    """BASELINE C4 inputs from seed 4, on the CPU: X = randn([8192, 3072]).bf16();
+    W_gate, W_up = 0.02 * randn([12288, 3072]) each, quantized per output row
+    (s_n = amax_n / 127, Wq = rint(W / s_n).clamp(-127, 127)). Shared with
+    tests/test_gpu_configs.py, which must draw the same bytes."""
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(8192, 3072, generator=g).to(torch.bfloat16)
+    ws = []
+    for _ in range(2):
+        w = 0.02 * torch.randn(12288, 3072, generator=g)
+        s = w.abs().amax(dim=1) / 127.0
+        q = torch.round(w / s[:, None]).clamp(-127, 127).to(torch.int8)
+        ws.append((q, s.float().contiguous()))
+    return x, ws
+
+
+def c4_digests():
+    x, ((wg, gs), (wu, us)) = c4_inputs()
+    # rowwise quant, the comfy_kitchen formula in torch ops (as quant_rows)
+    xf = x.float()
+    scale = torch.clamp(xf.abs().amax(dim=1) / 127.0, min=1e-30)
+    s = scale.to(torch.bfloat16)
+    s = torch.where(s == 0, torch.full_like(s, torch.finfo(torch.bfloat16).tiny), s)
+    q = torch.clamp(torch.round((xf / s.float()[:, None]).to(torch.bfloat16).float()),
+                    -128, 127).to(torch.int8)
+    gate = (torch._int_mm(q, wg.t()).float() * (gs[None, :] * scale[:, None])).to(torch.bfloat16)
+    up = (torch._int_mm(q, wu.t()).float() * (us[None, :] * scale[:, None])).to(torch.bfloat16)
+    y = F.silu(gate) * up
+    return {"c4_seed": 4, "c4_q_sha256": sha(q.numpy()), "c4_scale_sha256": sha(scale.numpy()),
+            "c4_pair_bf16_sha256": sha(y.view(torch.int16).numpy())}
 
 
 if __name__ == "__main__":

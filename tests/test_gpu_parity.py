@@ -433,7 +433,7 @@ def test_i8_mlp_bridge_prequant_exact(dev, M, K, F, tile_rows):
                                        tile_rows=tile_rows)
     fc1 = oi.epilogue_rowcolscale(oi.i8_matmul2d_nt(a.numpy(), w1.numpy()), rs.numpy(), cs.numpy(),
                                   bits16(bb))
-    silu = ops.act_table("silu", dev).cpu().numpy().view(np.uint16)
+    silu = oact.silu_table()
     rq, rsc = oi.quant_rowwise(ocr.swiglu_rot(fc1, silu), "bf16")
     assert q.shape == (M, F) and sc.shape == (M, 1)
     assert np.array_equal(q.cpu().numpy(), rq), f"bridge q {M}x{K} F{F} tile {tile_rows}"

@@ -123,21 +123,57 @@ def test_w8a16_forward_vs_oracle(dev, scaled):
 
 
 def test_krea2_project_exact(dev):
+    """Krea2 project: ConvRot rotation of every 256-group + rowwise quant
+    (the fused pass), then the pair kernel with the SiLU table, against the
+    oracle's rotate + quant and unfused pair chain (reference
+    _patches/krea2_ffn_pair.py:37-49)."""
+    from oracle import convrot as ocr
     g = gen(27)
-    x = torch.randn(1, 200, 512, generator=g).to(torch.bfloat16)
-    wg, wu = _i8((384, 512), g), _i8((384, 512), g)
-    gs, us = torch.rand(384, generator=g) * 0.02, torch.rand(384, generator=g) * 0.02
+    K, F = 512, 384
+    x = torch.randn(1, 200, K, generator=g).to(torch.bfloat16)
+    wg, wu = _i8((F, K), g), _i8((F, K), g)
+    gs, us = torch.rand(F, generator=g) * 0.02, torch.rand(F, generator=g) * 0.02
     int8_linear._act_cache = None
     out = krea2_ffn_pair.project(x.to(dev), (wg.to(dev), gs.to(dev)), (wu.to(dev), us.to(dev)))
-    assert out.shape == (1, 200, 384)
-    # the unfused chain with the same device's bf16 SiLU (table of F.silu on dev)
-    q, rs = oi.quant_rowwise(bits16(x.reshape(-1, 512)))
-    gb = oi.epilogue_rowcolscale(oi.i8_matmul2d_nt(q, wg.numpy()), rs, gs.numpy())
-    ub = oi.epilogue_rowcolscale(oi.i8_matmul2d_nt(q, wu.numpy()), rs, us.numpy())
-    silu_dev = ops.act_table("silu", dev).cpu().numpy().view(np.uint16)
-    act = oact.apply_table(silu_dev, gb)
-    ref = bits16(torch.from_numpy(bf16_to_f32(act) * bf16_to_f32(ub)).to(torch.bfloat16))
-    assert_bits_equal(bits16(out.reshape(-1, 384)), ref, "krea2 project")
+    assert out.shape == (1, 200, F)
+    xb = bits16(x.reshape(200, K)).reshape(200, K // 256, 1, 256)
+    q, rs = ocr.merge_rot_quant(xb)
+    ref = op.krea2_pair(q, wg.numpy(), wu.numpy(), np.asarray(rs).reshape(-1), gs.numpy(),
+                        us.numpy())
+    assert_bits_equal(bits16(out.reshape(-1, F)), ref, "krea2 project (ConvRot)")
+
+
+def test_krea2_candidate_routes_convrot_layers(dev):
+    """The SwiGLU seam on ConvRot group-256 INT8 layers: down(project(x))
+    with the pair output bit-exact against the oracle chain."""
+    from oracle import convrot as ocr
+    g = gen(31)
+    K, F = 768, 256
+    x = torch.randn(1, 96, K, generator=g).to(torch.bfloat16)
+    wg, wu = _i8((F, K), g), _i8((F, K), g)
+    gs, us = torch.rand(F, generator=g) * 0.02, torch.rand(F, generator=g) * 0.02
+
+    class QT:
+        _layout_cls = "TensorWiseINT8Layout"
+
+        def __init__(self, q, s):
+            self._qdata = q
+            self._params = types.SimpleNamespace(scale=s, convrot=True, convrot_groupsize=256,
+                                                 transposed=False)
+
+    def lin(q, s):
+        return types.SimpleNamespace(weight=QT(q.to(dev), s.to(dev)), bias=None,
+                                     weight_function=[], bias_function=[])
+    seen = []
+    mod = types.SimpleNamespace(gate=lin(wg, gs), up=lin(wu, us),
+                                down=lambda h: seen.append(h) or "down")
+    int8_linear._act_cache = None
+    with torch.no_grad():
+        assert krea2_ffn_pair.candidate(lambda self, x: "original", mod, x.to(dev)) == "down"
+    q, rs = ocr.merge_rot_quant(bits16(x.reshape(96, K)).reshape(96, K // 256, 1, 256))
+    ref = op.krea2_pair(q, wg.numpy(), wu.numpy(), np.asarray(rs).reshape(-1), gs.numpy(),
+                        us.numpy())
+    assert_bits_equal(bits16(seen[0].reshape(-1, F)), ref, "krea2 candidate")
 
 
 def test_moss_project_exact(dev):
@@ -201,7 +237,7 @@ def test_o_proj_prequant_and_swiglu_forward_exact(dev):
                                 bias_function=[])
     y = int8_linear._try_int8_swiglu_forward(lin, xf.to(dev))
     assert y.shape == (2, 35, N)
-    silu_dev = ops.act_table("silu", dev).cpu().numpy().view(np.uint16)
+    silu_dev = oact.silu_table()
     rq2, rs2 = oi.quant_rowwise(ocr.swiglu_rot(bits16(xf.reshape(70, 2 * F)), silu_dev), "bf16")
     ref2 = oi.epilogue_rowcolscale(oi.i8_matmul2d_nt(rq2, w2.numpy()), rs2.reshape(-1), ws.numpy())
     assert_bits_equal(bits16(y.reshape(70, N)), ref2, "swiglu fc2 patch")
@@ -276,7 +312,7 @@ def test_mlp_bridge_route_exact(dev):
     xq, xs = oi.quant_rowwise(bits16(x), "bf16")
     h = oi.epilogue_rowcolscale(oi.i8_matmul2d_nt(xq, w1.numpy()), xs.reshape(-1), s1.numpy(),
                                 bits16(b1))
-    silu = ops.act_table("silu", dev).cpu().numpy().view(np.uint16)
+    silu = oact.silu_table()
     rq, rs = oi.quant_rowwise(ocr.swiglu_rot(h, silu), "bf16")
     ref = oi.epilogue_rowcolscale(oi.i8_matmul2d_nt(rq, w2.numpy()), rs.reshape(-1), s2.numpy(),
                                   bits16(b2))
