@@ -37,6 +37,8 @@ _SIGNATURES = {
     "c4q_i8_swiglu_rot_quant": [_P, _I64, _I64, _P, _P, _P, _P],
     "c4q_i8_mlp_bridge_prequant": [_P, _I64, _P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _I64,
                                    _P, _P, _P, _P, _P],
+    "c4q_i8_mlp_bridge_prequant_noalloc": [_P, _I64, _P, _I64, _P, _P, _P, _P, _I64, _I64, _I64,
+                                           _P, _P, _P],
     "c4q_i8_merge_rot_quant": [_P, _I64, _I64, _I64, _I64, _I, _P, _P, _P],
     "c4q_i8_swiglu_rot": [_P, _I64, _I64, _P, _P, _P],
     "c4q_f8_gemm_nt_scaled": [_P, _I64, _P, _I64, _P, _I, _I64, _P, _I, _P, _I, _P, _P, _I,

@@ -1,5 +1,6 @@
 // INT8 W8A8 entry points: raw int32, per-tensor and per-channel fused
 // epilogues, and the fused gate/up FFN pair.
+#include <mutex>
 #include "launch.hpp"
 
 using namespace c4q;
@@ -328,6 +329,67 @@ extern "C" int c4q_i8_mlp_bridge_prequant(const int8_t* a, int64_t lda, const in
     if (st != C4Q_OK) return st;
   }
   return C4Q_OK;
+}
+
+// ---- MLP bridge without allocations ---------------------------------------
+// The bridge's FC1 staging (`wide`, and `rot` for F > 15360) lives in one
+// file-scope device array per GPU instead of caller scratch. Host code never
+// passes the array's name to a kernel or a copy: it passes the address that
+// hipGetSymbolAddress returns for the current device, looked up once per
+// device on the entry point's first call there.
+static __device__ __align__(256) uint16_t scratch[C4Q_BRIDGE_SCRATCH_BYTES / 2];
+
+namespace {
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[64] = {nullptr};
+
+int bridge_scratch(uint16_t** out, const char* what) {
+  int dev = -1;
+  C4Q_REQUIRE(hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64, C4Q_ERR_HIP,
+              "%s: no current HIP device (or device index >= 64)", what);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    C4Q_REQUIRE(e == hipSuccess && p != nullptr, C4Q_ERR_HIP,
+                "%s: hipGetSymbolAddress(scratch) failed on device %d: %s", what, dev,
+                hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = static_cast<uint16_t*>(g_scratch_ptr[dev]);
+  return C4Q_OK;
+}
+}  // namespace
+
+extern "C" int c4q_i8_mlp_bridge_prequant_noalloc(const int8_t* a, int64_t lda, const int8_t* w1,
+                                                  int64_t ldw, const float* row_scale,
+                                                  const float* col_scale, const uint16_t* bias,
+                                                  const uint16_t* silu_table, int64_t M,
+                                                  int64_t K, int64_t W, int8_t* q, float* scales,
+                                                  void* stream) {
+  const char* what = "c4q_i8_mlp_bridge_prequant_noalloc";
+  C4Q_REQUIRE(M >= 0 && K >= 0 && W > 0 && W % 512 == 0, C4Q_ERR_SHAPE,
+              "%s: need W = 2F > 0 with F a multiple of 256 (W=%lld)", what, (long long)W);
+  if (M == 0) return C4Q_OK;
+  const int64_t F = W / 2;
+  const bool one_pass = F * 2 <= 30 * 1024;
+  // staging bytes per FC1 row: the bf16 row [2F], plus its rotated half [F]
+  // on the two-pass route
+  const int64_t row_bytes = one_pass ? 4 * F : 6 * F;
+  const int64_t fit = C4Q_BRIDGE_SCRATCH_BYTES / row_bytes;
+  int64_t rows = M <= fit ? M : fit / 128 * 128;
+  C4Q_REQUIRE(rows >= 1 && (rows == M || rows >= 128), C4Q_ERR_SHAPE,
+              "%s: a chunk of 128 FC1 rows of F=%lld needs %lld bytes of staging, more than the "
+              "%lld-byte scratch; use c4q_i8_mlp_bridge_prequant with caller scratch",
+              what, (long long)F, (long long)(128 * row_bytes),
+              (long long)C4Q_BRIDGE_SCRATCH_BYTES);
+  uint16_t* base = nullptr;
+  const int st = bridge_scratch(&base, what);
+  if (st != C4Q_OK) return st;
+  uint16_t* wide = base;
+  uint16_t* rot = one_pass ? nullptr : base + rows * W;
+  return c4q_i8_mlp_bridge_prequant(a, lda, w1, ldw, row_scale, col_scale, bias, silu_table, M, K,
+                                    W, rows, wide, rot, q, scales, stream);
 }
 
 extern "C" int c4q_i8_ffn_pair(const int8_t* a, int64_t lda, const int8_t* w_gate,

@@ -308,6 +308,34 @@ def i8_mlp_bridge_prequant(a_i8, fc1_weight, row_scale, fc1_col_scale, fc1_bias=
     return q, scales
 
 
+def i8_mlp_bridge_prequant_noalloc(a_i8, fc1_weight, row_scale, fc1_col_scale, fc1_bias=None):
+    """i8_mlp_bridge_prequant with FC1's staging in the library's own
+    per-GPU array (64 MiB) instead of torch-allocated scratch: the outputs
+    q [M, F] and scales [M, 1] are allocated here, nothing else. Rows run in
+    chunks of as many 128-row blocks as the array holds. Calls that overlap
+    on one GPU (other streams or threads) race on the array."""
+    dev, lda, ldw = _i8_operands(a_i8, fc1_weight)
+    _req(a_i8.is_contiguous() and fc1_weight.is_contiguous(),
+         "activation and FC1 weight must be contiguous 2D tensors")
+    M, K = a_i8.shape
+    W = fc1_weight.size(0)
+    _req(M > 64 and W > 0 and W % 512 == 0, "bridge requires M > 64 and F divisible by 256")
+    _dev(row_scale, fc1_col_scale, fc1_bias)
+    _vec(row_scale, M, torch.float32, "row_scale")
+    _vec(fc1_col_scale, W, torch.float32, "fc1_col_scale")
+    bias = _bias_bf16(fc1_bias, W)
+    F = W // 2
+    q = torch.empty((M, F), dtype=torch.int8, device=dev)
+    scales = torch.empty((M, 1), dtype=torch.float32, device=dev)
+    silu = act_table("silu", dev)
+    with _on(dev):
+        _lib.call("c4q_i8_mlp_bridge_prequant_noalloc", a_i8.data_ptr(), lda,
+                  fc1_weight.data_ptr(), ldw, row_scale.data_ptr(), fc1_col_scale.data_ptr(),
+                  bias.data_ptr() if bias is not None else None, silu.data_ptr(), M, K, W,
+                  q.data_ptr(), scales.data_ptr(), _stream(dev))
+    return q, scales
+
+
 def i8_merge_rot_quant(x, rotate=True):
     """x [B,H,S,D] bf16 (attention layout) -> (q [B*S, H*D] int8,
     scales [B*S, 1] fp32): head merge, ConvRot rotation of every 256-element

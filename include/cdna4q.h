@@ -170,6 +170,29 @@ int c4q_i8_mlp_bridge_prequant(const int8_t* a, int64_t lda, const int8_t* w1, i
                                int64_t K, int64_t W, int64_t tile_rows, uint16_t* wide,
                                uint16_t* rot, int8_t* q, float* scales, void* stream);
 
+/* Bytes of the per-GPU device array that c4q_i8_mlp_bridge_prequant_noalloc
+ * stages FC1 rows in (64 MiB, held by each GPU the library runs on until the
+ * process ends). */
+#define C4Q_BRIDGE_SCRATCH_BYTES (64ll << 20)
+
+/* c4q_i8_mlp_bridge_prequant without caller scratch and without any device
+ * allocation: FC1's bf16 rows (and, for F > 15360, their rotated halves) are
+ * staged in the library's own C4Q_BRIDGE_SCRATCH_BYTES array on the current
+ * device, in chunks of as many whole 128-row blocks as fit (all M rows at
+ * once when they fit). Same outputs q [M, F] int8 and scales [M] fp32, byte
+ * for byte, as c4q_i8_mlp_bridge_prequant. Rejects (C4Q_ERR_SHAPE) an F whose
+ * 128-row chunk does not fit the array (F > 87381). Calls on one GPU share
+ * its array: calls that overlap in time on one GPU (different streams, or
+ * different host threads without ordering) race on it.
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). */
+int c4q_i8_mlp_bridge_prequant_noalloc(const int8_t* a, int64_t lda, const int8_t* w1,
+                                       int64_t ldw, const float* row_scale,
+                                       const float* col_scale, const uint16_t* bias,
+                                       const uint16_t* silu_table, int64_t M, int64_t K,
+                                       int64_t W, int8_t* q, float* scales, void* stream);
+
 /* torch._scaled_mm fp8 route: D[M,N] = out_dtype(((f32(A@B^T) * scale_a)
  * * scale_b) * scale_result + f32(bias[n])). A [M,K] and B [N,K] are e4m3fn
  * bytes; scale_result and bias may be NULL.
