@@ -24,6 +24,7 @@ timed region; weights are random-init N(0, 0.02) quantized the way each
 config specifies.
 """
 import argparse
+import hashlib
 import importlib.util
 import json
 import os
@@ -510,9 +511,28 @@ COPY_BYTES = 512 * 1024 * 1024
 TRAFFIC_FILE = ROOT / "profiles" / "w8a16_gemm_c2_qkv_traffic.json"
 QKV_KERNEL_KEY = "OpW8A16"
 PMC_CALLS = 3
+SOURCE_FILES = ("comfyui-applesilicon-optimized_amd/csrc", "include")
 
 
-def pmc_target(torch, ops, dev):
+def source_hash():
+    """sha256 (first 16 hex digits) of the kernel sources: every file under
+    csrc/ and include/, in name order. A profile stamped with another hash
+    measured another build."""
+    h = hashlib.sha256()
+    for d in SOURCE_FILES:
+        for f in sorted((ROOT / d).rglob("*")):
+            if f.is_file() and f.suffix in (".hip", ".hpp", ".cpp", ".h"):
+                h.update(f.relative_to(ROOT).as_posix().encode())
+                h.update(f.read_bytes())
+    return h.hexdigest()[:16]
+
+
+def pmc_target(torch, ops, dev, which="C2"):
+    """Counter target: the copy calibration, then PMC_CALLS calls of the C2
+    QKV W8A16 GEMM (which = "C2"), or of each headline kernel in turn
+    (which = "KERNELS": C2 QKV, C2 out-proj, C1 fused_cs, C3 up, C3 down,
+    C4 pair, skinny M=4 N=18432) for per-kernel counters."""
+    log(f"pmc target {which}: copy calibration")
     src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=dev).uniform_()
     dst = torch.empty_like(src)
     for _ in range(3):
@@ -523,6 +543,46 @@ def pmc_target(torch, ops, dev):
     q, s, b = layers[0]
     for _ in range(PMC_CALLS):
         ops.w8a16_linear(x, q, s, b)
+    torch.cuda.synchronize()
+    if which == "C2":
+        return
+    q, s, b = layers[1]
+    for _ in range(PMC_CALLS):
+        ops.w8a16_linear(x, q, s, b)
+    del x, layers
+    g = torch.Generator(device=dev).manual_seed(1)
+    a = torch.randint(-127, 128, (1024, 3072), generator=g, device=dev, dtype=torch.int8)
+    w = torch.randint(-127, 128, (3072, 3072), generator=g, device=dev, dtype=torch.int8)
+    rs = 0.005 + 0.015 * torch.rand(1024, generator=g, device=dev)
+    cs = 0.0005 + 0.0015 * torch.rand(3072, generator=g, device=dev)
+    for _ in range(PMC_CALLS):
+        ops.i8_matmul2d_nt_fused_cs(a, w, rs, cs)
+    torch.cuda.synchronize()
+    log("pmc target: C3")
+    for K, N in ((5120, 13824), (13824, 5120)):
+        x = torch.randn(16384, K, generator=g, device=dev).to(torch.bfloat16)
+        wq, ws = fp8_pertensor(torch, 0.02 * torch.randn(N, K, generator=g, device=dev))
+        xq, xs = ops.fp8_quant_pertensor(x)
+        for _ in range(PMC_CALLS):
+            ops.scaled_mm(xq, wq.t(), out_dtype=torch.bfloat16, scale_a=xs, scale_b=ws)
+        torch.cuda.synchronize()
+        del x, wq, xq
+    log("pmc target: C4")
+    q8 = torch.randint(-127, 128, (8192, 3072), generator=g, device=dev, dtype=torch.int8)
+    wg = torch.randint(-127, 128, (12288, 3072), generator=g, device=dev, dtype=torch.int8)
+    wu = torch.randint(-127, 128, (12288, 3072), generator=g, device=dev, dtype=torch.int8)
+    rs = torch.rand(8192, generator=g, device=dev) * 0.01
+    gs = torch.rand(12288, generator=g, device=dev) * 0.002
+    silu = ops.act_table("silu", dev)
+    for _ in range(PMC_CALLS):
+        ops.ffn_pair(q8, wg, wu, rs, gs, gs, silu, None)
+    torch.cuda.synchronize()
+    log("pmc target: skinny")
+    xs4 = torch.randn(4, 3072, generator=g, device=dev).to(torch.bfloat16)
+    wq, ws = fp8_pertensor(torch, 0.02 * torch.randn(18432, 3072, generator=g, device=dev))
+    bs = torch.zeros(18432, dtype=torch.bfloat16, device=dev)
+    for _ in range(PMC_CALLS):
+        ops.w8a16_linear(xs4, wq, ws, bs)
     torch.cuda.synchronize()
 
 
@@ -556,6 +616,7 @@ def pmc_summarize(fetch_dir, write_dir):
     M, K, N = 9216, 3072, 9216
     algo = M * K * 2 + N * K + N * 2 + 4 + M * N * 2   # X bf16 + W fp8 + bias bf16 + scale + Y bf16
     out["traffic_bytes"] = out["FETCH_SIZE"]["qkv_bytes"] + out["WRITE_SIZE"]["qkv_bytes"]
+    out["source_hash"] = source_hash()
     out["algorithmic_bytes"] = algo
     out["kernel"] = "W8A16 GEMM fused-QKV 9216x3072 -> 9216 (C2), main + tail launch"
     TRAFFIC_FILE.write_text(json.dumps(out, indent=1) + "\n")
@@ -563,8 +624,15 @@ def pmc_summarize(fetch_dir, write_dir):
 
 
 def load_traffic():
+    """HBM traffic per C2 QKV call from the committed counter summary, or
+    None when that summary measured another build (its source hash differs
+    from the sources of this one) or is missing."""
     try:
         t = json.loads(TRAFFIC_FILE.read_text())
+        if t.get("source_hash") != source_hash():
+            log("roofline.traffic: the counter summary was measured on other kernel sources; "
+                "reporting null")
+            return None
         return round(t["traffic_bytes"])
     except (OSError, KeyError, ValueError):
         return None
@@ -579,13 +647,19 @@ def main():
                     help="comma list of configs to run (C2 is always run); MOSS_BF16, "
                          "WAN_FP16, CONVROT and H3 time the widened rows (not BASELINE configs)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--pmc-target", action="store_true",
-                    help="run the copy calibration and the C2 QKV kernel for rocprofv3 --pmc")
+    ap.add_argument("--pmc-target", nargs="?", const="C2", choices=("C2", "KERNELS"),
+                    help="run the copy calibration and the C2 QKV kernel (or every headline "
+                         "kernel: KERNELS) for rocprofv3 --pmc")
+    ap.add_argument("--source-hash", action="store_true",
+                    help="print the kernel-source hash that profiles are stamped with")
     ap.add_argument("--pmc-summarize", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="write the traffic summary from two rocprofv3 --pmc output dirs")
     args = ap.parse_args()
     if args.pmc_summarize:
         pmc_summarize(*args.pmc_summarize)
+        return
+    if args.source_hash:
+        print(source_hash())
         return
     if args.gpus != 1:
         log(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -598,7 +672,7 @@ def main():
 
     dev = torch.device("cuda", 0)
     if args.pmc_target:
-        pmc_target(torch, ops, dev)
+        pmc_target(torch, ops, dev, args.pmc_target)
         return
     only = {c.strip().upper() for c in args.only.split(",") if c.strip()}
     per = {}
@@ -654,6 +728,7 @@ def main():
                      "traffic": load_traffic(),
                      "kernel": c2["kernel"]},
         "cpu_baseline": cpu,
+        "source_hash": source_hash(),
         "per_config": per,
     }
     print(json.dumps(line), flush=True)
