@@ -348,11 +348,13 @@ struct OpW8A16 {
       dequant4<BF16, HAS_SCALE>((uint32_t)f.q[j].w, ws, o[6], o[7]);
       const i32x4 b0 = {(int)o[0], (int)o[1], (int)o[2], (int)o[3]};
       const i32x4 b1 = {(int)o[4], (int)o[5], (int)o[6], (int)o[7]};
+      // both K halves of a block go into the same accumulator, first half
+      // first; the other blocks' MFMAs sit between the two, so an MFMA never
+      // waits on the one issued right before it
 #pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        acc[i][j] = mfma(f.a[0][i], b0, acc[i][j]);
-        acc[i][j] = mfma(f.a[1][i], b1, acc[i][j]);
-      }
+      for (int i = 0; i < TM; ++i) acc[i][j] = mfma(f.a[0][i], b0, acc[i][j]);
+#pragma unroll
+      for (int i = 0; i < TM; ++i) acc[i][j] = mfma(f.a[1][i], b1, acc[i][j]);
     }
   }
 };
