@@ -991,6 +991,14 @@ gemm_tile_kernel(GemmShape sh, Src2 sa, Src2 sb, const float* b_scale, Epi epi) 
   // next stage is visible (its first fragments load under the last step's
   // MFMAs) and the stage just read is free to refill.
   const int ra0 = wm * (TM * 32), rb0i = wn * (TN * 32);
+  // Eight waves (two per SIMD) and at least four K steps per stage: the
+  // upper four waves issue their copies after the last step's MFMAs instead
+  // of right after the barrier, so that on every SIMD one wave feeds the
+  // matrix pipe while the other waits for the address unit to take its
+  // copies (int8 128-K stages: +1-5 %). With two steps per stage (fp8,
+  // W8A16) that delay is half a stage of the copies' latency budget in the
+  // two-stage ring, and costs 14 % (fp8).
+  const bool late = WM * WN == 8 && S >= 4 && wave >= 4;
   using Frag = typename Op::template Frag<TM, TN>;
   Frag fr[2];
   uint8_t* strip = smem + RING + wave * kStrip;
@@ -1034,7 +1042,7 @@ gemm_tile_kernel(GemmShape sh, Src2 sa, Src2 sb, const float* b_scale, Epi epi) 
           wait_vm<(NBUF - 2) * kPerStage>();   // this wave's copies of stage gs+1 landed
           if constexpr (kEarly) early.settle();
           stage_barrier();                     // ... and every wave's; stage gs fully read
-          issue_next(cur);                     // refill with stage gs+NBUF
+          if (!late) issue_next(cur);          // refill with stage gs+NBUF
           if (has_next) Op::template frags<TM, TN>(fr[0], nxt, nxt + BM * SA, ra0, rb0i, 0);
         } else {
           Op::template frags<TM, TN>(fr[(s + 1) & 1], cur, cur + BM * SA, ra0, rb0i, s + 1);
@@ -1044,6 +1052,10 @@ gemm_tile_kernel(GemmShape sh, Src2 sa, Src2 sb, const float* b_scale, Epi epi) 
           __builtin_amdgcn_sched_barrier(0);
         }
         Op::template mma<TM, TN>(fr[s & 1], acc, ws);
+        if (s == S - 1 && late) {
+          __builtin_amdgcn_sched_barrier(0);
+          issue_next(cur);
+        }
       }
       ++gs;
     };
