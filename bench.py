@@ -514,6 +514,74 @@ PMC_CALLS = 3
 SOURCE_FILES = ("comfyui-applesilicon-optimized_amd/csrc", "include")
 
 
+# ------------------------------------------- vendor library, same shapes ---
+# Not part of the metric: torch's own ROCm route (hipBLASLt) on the GEMM
+# shapes of C1-C4, timed in the same process as this package's kernels, so
+# the two can be compared on one box at one clock. The vendor calls do the
+# GEMM only: int32 out for INT8 (no row/column scales, no SwiGLU pair
+# epilogue), a bf16 x bf16 weight for C2 (no fp8 decode).
+
+def bench_vendor(torch, ops, dev, steps, warmup):
+    g = torch.Generator(device=dev).manual_seed(11)
+    F = torch.nn.functional
+
+    def i8(*s):
+        return torch.randint(-127, 128, s, generator=g, device=dev, dtype=torch.int8)
+
+    def timed(fn):
+        _, kern = Timer(torch).run(lambda p: marked(p, fn), steps, warmup)
+        return kern
+
+    out = {}
+    # C1: INT8 1024x3072 -> 3072
+    a, w = i8(1024, 3072), i8(3072, 3072)
+    rs = torch.rand(1024, generator=g, device=dev) * 0.01
+    cs = torch.rand(3072, generator=g, device=dev) * 0.001
+    fl = 2.0 * 1024 * 3072 * 3072
+    t_v = timed(lambda: torch._int_mm(a, w.t()))
+    t_o = timed(lambda: ops.i8_matmul2d_nt_fused_cs(a, w, rs, cs))
+    out["C1"] = {"vendor_us": t_v * 1e6, "ours_us": t_o * 1e6, "vendor_tops": fl / t_v / 1e12,
+                 "ours_tops": fl / t_o / 1e12, "vendor_op": "torch._int_mm (int32 out)",
+                 "ours_op": "i8_matmul2d_nt_fused_cs (bf16 out, row/col scales)"}
+    del a, w
+    # C2 QKV: 9216x3072 -> 9216
+    x, layers = make_c2(torch, dev, Ns=(9216,))
+    q, s, b = layers[0]
+    wb = (q.float() * s).to(torch.bfloat16)
+    fl = 2.0 * 9216 * 3072 * 9216
+    t_v = timed(lambda: F.linear(x, wb, b))
+    t_o = timed(lambda: ops.w8a16_linear(x, q, s, b))
+    out["C2_QKV"] = {"vendor_us": t_v * 1e6, "ours_us": t_o * 1e6, "vendor_tflops": fl / t_v / 1e12,
+                     "ours_tflops": fl / t_o / 1e12, "vendor_op": "F.linear bf16 x bf16 + bias",
+                     "ours_op": "w8a16_linear (fp8 weight decoded in registers)"}
+    del x, layers, q, wb
+    # C3 up / down: fp8 per-tensor
+    one = torch.ones((), device=dev)
+    for name, K, N in (("C3_up", 5120, 13824), ("C3_down", 13824, 5120)):
+        a = (torch.randn(16384, K, generator=g, device=dev) * 30).clamp(-448, 448).to(torch.float8_e4m3fn)
+        w = (torch.randn(N, K, generator=g, device=dev) * 30).clamp(-448, 448).to(torch.float8_e4m3fn)
+        fl = 2.0 * 16384 * N * K
+        t_v = timed(lambda: torch._scaled_mm(a, w.t(), scale_a=one, scale_b=one, out_dtype=torch.bfloat16))
+        t_o = timed(lambda: ops.scaled_mm(a, w.t(), out_dtype=torch.bfloat16, scale_a=one, scale_b=one))
+        out[name] = {"vendor_us": t_v * 1e6, "ours_us": t_o * 1e6, "vendor_tflops": fl / t_v / 1e12,
+                     "ours_tflops": fl / t_o / 1e12, "vendor_op": "torch._scaled_mm (bf16 out)",
+                     "ours_op": "scaled_mm (bf16 out)"}
+        del a, w
+    # C4: INT8 8192x3072 -> 2x12288
+    a, wg, wu = i8(8192, 3072), i8(12288, 3072), i8(12288, 3072)
+    wcat = torch.cat([wg, wu], 0)
+    rs = torch.rand(8192, generator=g, device=dev) * 0.01
+    gs = torch.rand(12288, generator=g, device=dev) * 0.002
+    silu = ops.act_table("silu", dev)
+    fl = 2.0 * 8192 * 24576 * 3072
+    t_v = timed(lambda: torch._int_mm(a, wcat.t()))
+    t_o = timed(lambda: ops.ffn_pair(a, wg, wu, rs, gs, gs, silu, None))
+    out["C4"] = {"vendor_us": t_v * 1e6, "ours_us": t_o * 1e6, "vendor_tops": fl / t_v / 1e12,
+                 "ours_tops": fl / t_o / 1e12, "vendor_op": "torch._int_mm over [gate; up] (int32 out)",
+                 "ours_op": "ffn_pair (SiLU(gate) * up, bf16 out)"}
+    return out
+
+
 def source_hash():
     """sha256 (first 16 hex digits) of the kernel sources: every file under
     csrc/ and include/, in name order. A profile stamped with another hash
@@ -654,6 +722,9 @@ def main():
                     help="print the kernel-source hash that profiles are stamped with")
     ap.add_argument("--pmc-summarize", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="write the traffic summary from two rocprofv3 --pmc output dirs")
+    ap.add_argument("--vendor", action="store_true",
+                    help="time torch's hipBLASLt route on the C1-C4 GEMM shapes next to this "
+                         "package's kernels (one JSON line; not the metric)")
     args = ap.parse_args()
     if args.pmc_summarize:
         pmc_summarize(*args.pmc_summarize)
@@ -673,6 +744,10 @@ def main():
     dev = torch.device("cuda", 0)
     if args.pmc_target:
         pmc_target(torch, ops, dev, args.pmc_target)
+        return
+    if args.vendor:
+        res = bench_vendor(torch, ops, dev, args.steps, args.warmup)
+        print(json.dumps({"vendor_comparison": res, "source_hash": source_hash()}), flush=True)
         return
     only = {c.strip().upper() for c in args.only.split(",") if c.strip()}
     per = {}
