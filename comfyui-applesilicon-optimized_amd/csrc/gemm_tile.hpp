@@ -170,6 +170,17 @@ struct DirectLoad {
       voff[j] = (int)(src * ld_bytes) + kofs;
     }
   }
+  // Copy J of issue() alone, for schedules that spread a stage's copies.
+  template <int J>
+  __device__ __forceinline__ void issue_one(u32x4 r0, u32x4 r1, uint8_t* lds, int kb,
+                                            int k_bytes) const {
+    static_assert(J >= 0 && J < kInstr, "copy index");
+    const bool in_k = kb + kofs < k_bytes;
+    const int rq = row0 + RPI * (wv + kWaves * J);
+    const u32x4 rs = (PAIR && ((rq >> 5) & 1)) ? r1 : r0;
+    const int vo = PAIR ? voff[PAIR ? J : 0] : voff[0] + J * step;
+    lds_dma16(rs, lds + rq * ROWB, in_k ? vo : kOOB, kb);
+  }
   // Copy K bytes [kb, kb + ROWB) of every row into `lds`; bytes at or past
   // k_bytes read zeros.
   __device__ __forceinline__ void issue(u32x4 r0, u32x4 r1,
@@ -216,6 +227,15 @@ __device__ __forceinline__ void dequant4(uint32_t w, float s, uint32_t& lo, uint
     f16x2 ha = {(_Float16)a.x, (_Float16)a.y};
     f16x2 hb = {(_Float16)b.x, (_Float16)b.y};
     lo = bitcast<uint32_t>(ha); hi = bitcast<uint32_t>(hb);
+  }
+}
+
+// Calls f(std::integral_constant<int, Q>{}) for Q = Q0 .. Q1-1.
+template <int Q0, int Q1, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (Q0 < Q1) {
+    f(std::integral_constant<int, Q0>{});
+    static_for<Q0 + 1, Q1>(f);
   }
 }
 
@@ -293,6 +313,20 @@ struct OpF8T {
       for (int j = 0; j < TN; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.a[i], f.b[j], acc[i][j], 0, 0,
                                                                     0, 0, 0, 0);
+  }
+  // One fragment block (Q < TM: A block Q, else B block Q - TM) and one
+  // MFMA, for schedules that interleave them with other work.
+  template <int TM, int TN, int Q>
+  __device__ __forceinline__ static void frag_one(Frag<TM, TN>& f, const uint8_t* sa,
+                                                  const uint8_t* sb, int ra0, int rb0, int s) {
+    const int lane = threadIdx.x & 63, lr = lane & 31, h = lane >> 5;
+    if constexpr (Q < TM) f.a[Q] = pair_chunks<SA>(sa, ra0 + Q * 32 + lr, 4 * s + 2 * h);
+    else f.b[Q - TM] = pair_chunks<SB>(sb, rb0 + (Q - TM) * 32 + lr, 4 * s + 2 * h);
+  }
+  template <int TM, int TN, int I, int J>
+  __device__ __forceinline__ static void mma_one(const Frag<TM, TN>& f, Acc (&acc)[TM][TN]) {
+    acc[I][J] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.a[I], f.b[J], acc[I][J], 0, 0,
+                                                                0, 0, 0, 0);
   }
 };
 // The fp8 policy always stages 128 K (two K steps; the pipeline needs an
@@ -902,6 +936,14 @@ __device__ __forceinline__ void stage_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// stage_barrier with the LDS wait issued as a builtin, so the compiler's
+// wait insertion knows every LDS read before it has completed and adds no
+// waits of its own for them afterwards.
+__device__ __forceinline__ void stage_barrier_tracked() {
+  __builtin_amdgcn_s_waitcnt(0xc07f);    // lgkmcnt(0); vmcnt and expcnt unconstrained
+  asm volatile("s_barrier" ::: "memory");
+}
+
 // Bytes of one wave's epilogue strip.
 template <int TN, bool PAIR>
 constexpr int strip_bytes() { return Strip<(PAIR ? TN / 2 * 2 : TN) * 32>::kBytes; }
@@ -1211,6 +1253,174 @@ gemm_pingpong_kernel(GemmShape sh, Src2 sa, Src2 sb, const float* b_scale, Epi e
     }
   }
   if (grp == 0) stage_barrier();               // matches group 1's extra barrier
+  wait_vm<0>();    // zero-fill copies past the last tile still target the ring
+}
+
+// One wave per SIMD: a 256 x 256 tile of four waves of 128 x 128 (16
+// accumulator blocks, 256 accumulation registers each), 8-bit operands
+// through a ring of NBUF stages (fp8: two 128-K stages). With one wave on a
+// SIMD nothing covers a stall of that wave, so each K step is issued as one
+// interleaved stream: after every MFMA the wave issues the fragment reads
+// that the MFMA freed (fragments are refilled in place for the next step)
+// and, in the stage's last step, after the barrier that frees the stage's
+// buffer, one of its copies of stage gs + NBUF. LDS reads and copy issue
+// then run under the MFMAs. Each accumulator takes its K steps in the same
+// order as in gemm_tile_kernel, so the results are the same bits.
+// Measured on MI355X against the 8-wave kernel on the same tile (fp8, 16384
+// rows): per 128-K stage the MFMAs take ~2000 cycles, the fragment reads
+// add ~120 and the copy issue ~500 (the address unit is saturated while the
+// copies of a stage are issued in its last step); the epilogue is ~27k
+// cycles per tile and is not overlapped.
+template <class Op, int NBUF, bool PAIR, class Epi>
+__global__ void __launch_bounds__(256)
+gemm_w4_kernel(GemmShape sh, Src2 sa, Src2 sb, const float* b_scale, Epi epi) {
+  constexpr int BM = 256, BN = 256, WM = 2, WN = 2, NT = 256;
+  constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
+  static_assert(!PAIR || (TN % 2 == 0), "pair tiles need whole gate/up block pairs");
+  constexpr int SA = Op::SA, SB = Op::SB, S = Op::S;
+  constexpr int STAGE = BM * SA + BN * SB;
+  constexpr int RING = NBUF * STAGE;
+  constexpr int kStrip = strip_bytes<TN, PAIR>();
+  static_assert(NBUF >= 2 && RING + kStrip * WM * WN <= 160 * 1024, "LDS exceeds 160 KB");
+  using LA = DirectLoad<BM, SA, NT, false>;
+  using LB = DirectLoad<BN, SB, NT, PAIR>;
+  constexpr int kPerStage = LA::kInstr + LB::kInstr;     // copies per wave per stage
+  static_assert((NBUF - 1) * kPerStage < 64, "too many copies in flight for vmcnt");
+  constexpr int kMfma = TM * TN;                          // MFMAs per K step
+  static_assert(kMfma % kPerStage == 0, "one MFMA slot per copy");
+  constexpr int kCopyEvery = kMfma / kPerStage;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[RING + kStrip * WM * WN];
+
+  const int ntiles = sh.count;
+  const int G = (int)gridDim.x;
+  const int my_tiles = (ntiles - 1 - (int)blockIdx.x) / G + 1;
+  const Epi ep = epi.prepare();
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform
+  const int wm = wave / WN, wn = wave % WN;
+  const float ws = Op::prep_scale(b_scale);
+
+  LA la;
+  LB lb;
+  la.init(sa.ld_bytes, wave, 0);
+  lb.init(sb.ld_bytes, wave, 0);
+  constexpr int KS = Op::kStageK;
+  const int a_kb = (int)(sh.K * SA / KS), b_kb = (int)(sh.K * SB / KS);
+  const int nst = (int)((sh.K + KS - 1) / KS);
+
+  // Copy cursor: next stage to issue is stage ips of this workgroup's tile ij.
+  int ij = 0, ips = 0;
+  u32x4 ra, rb0, rb1;
+  auto tile_rsrc = [&](int j) __attribute__((always_inline)) {
+    const TileCoord tc = tile_at(sh, (int)blockIdx.x + j * G);
+    const int64_t m0 = (int64_t)tc.tm * BM;
+    const int64_t brow0 = PAIR ? ((int64_t)tc.tn * BN >> 1) : (int64_t)tc.tn * BN;
+    const int64_t bleft = (sb.rows - brow0) * sb.ld_bytes;
+    ra = dma_rsrc(sa.p0 + m0 * sa.ld_bytes, (sa.rows - m0) * sa.ld_bytes);
+    rb0 = dma_rsrc(sb.p0 + brow0 * sb.ld_bytes, bleft);
+    rb1 = PAIR ? dma_rsrc(sb.p1 + brow0 * sb.ld_bytes, bleft) : rb0;
+  };
+  // Copy C of the next stage (A copies first) into `buf`. Past this
+  // workgroup's last tile the copies read zeros (k limit 0), so every stage
+  // issues the same number of copies and the vmcnt arithmetic stays fixed.
+  auto issue_copy = [&](auto cc, uint8_t* buf, bool live) __attribute__((always_inline)) {
+    constexpr int C = decltype(cc)::value;
+    if constexpr (C < LA::kInstr) {
+      la.template issue_one<C>(ra, ra, buf, live ? ips * SA : 0, live ? a_kb : 0);
+    } else {
+      lb.template issue_one<C - LA::kInstr>(rb0, rb1, buf + BM * SA, live ? ips * SB : 0,
+                                            live ? b_kb : 0);
+    }
+  };
+  auto advance = [&]() __attribute__((always_inline)) {
+    if (ij < my_tiles && ++ips == nst) {
+      ips = 0;
+      if (++ij < my_tiles) tile_rsrc(ij);
+    }
+  };
+  tile_rsrc(0);
+
+  // prologue: stages 0 .. NBUF-1 in flight, stage 0 complete and visible
+#pragma unroll
+  for (int p = 0; p < NBUF; ++p) {
+    const bool live = ij < my_tiles;
+    static_for<0, kPerStage>([&](auto cc) { issue_copy(cc, smem + p * STAGE, live); });
+    advance();
+  }
+  wait_vm<(NBUF - 1) * kPerStage>();
+  stage_barrier();
+
+  const int ra0 = wm * (TM * 32), rb0i = wn * (TN * 32);
+  using Frag = typename Op::template Frag<TM, TN>;
+  Frag fr;
+  Op::template frags<TM, TN>(fr, smem, smem + BM * SA, ra0, rb0i, 0);
+  uint8_t* strip = smem + RING + wave * kStrip;
+  int gs = 0;                                   // stage counter over all tiles
+  for (int j = 0; j < my_tiles; ++j) {
+    typename Op::Acc acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int jj = 0; jj < TN; ++jj)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][jj][r] = 0;
+    // One stage. The fragments live in one set of registers, refilled in
+    // place for the next K step: A block i right after its last MFMA (row
+    // i, column TN-1), B block j right after its last (row TM-1, column j),
+    // so the reads of the next step run under this step's remaining MFMAs.
+    // The last step first waits for this wave's copies of stage gs + 1, then
+    // the barrier makes every wave's copies visible and frees stage gs's
+    // buffer (all its reads happened in earlier steps); that step's refills
+    // read stage gs + 1, and its copies refill the freed buffer with stage
+    // gs + NBUF.
+    auto stage = [&]() __attribute__((always_inline)) {
+      uint8_t* cur = smem + (gs % NBUF) * STAGE;
+      const uint8_t* nxt = smem + ((gs + 1) % NBUF) * STAGE;
+      static_for<0, S>([&](auto sc) {
+        constexpr int s = decltype(sc)::value;
+        constexpr bool kLast = s == S - 1;
+        if constexpr (kLast) {
+          wait_vm<(NBUF - 2) * kPerStage>();
+          stage_barrier_tracked();
+        }
+        const uint8_t* src = kLast ? nxt : cur;
+        constexpr int fs = kLast ? 0 : s + 1;
+        const bool live = ij < my_tiles;
+        static_for<0, kMfma>([&](auto qc) {
+          constexpr int q = decltype(qc)::value, i = q / TN, jn = q % TN;
+          Op::template mma_one<TM, TN, i, jn>(fr, acc);
+          if constexpr (jn == TN - 1)
+            Op::template frag_one<TM, TN, i>(fr, src, src + BM * SA, ra0, rb0i, fs);
+          if constexpr (i == TM - 1)
+            Op::template frag_one<TM, TN, TM + jn>(fr, src, src + BM * SA, ra0, rb0i, fs);
+          if constexpr (kLast && q % kCopyEvery == kCopyEvery - 1)
+            issue_copy(std::integral_constant<int, q / kCopyEvery>{}, cur, live);
+          __builtin_amdgcn_sched_barrier(0);
+        });
+        if constexpr (kLast) advance();
+      });
+      ++gs;
+    };
+    for (int st = 0; st < nst; ++st) stage();
+    // The epilogue parameters (raw, compact) are all issued first and waited
+    // for together with this wave's copies in flight (one drain per tile).
+    // Loaded one group at a time instead, each first use would wait for
+    // every copy in flight (memory counters complete in issue order).
+    const TileCoord tc = tile_at(sh, (int)blockIdx.x + j * G);
+    const int64_t wm0 = (int64_t)tc.tm * BM + wm * (TM * 32);
+    const int64_t wn0 = PAIR ? ((int64_t)tc.tn * BN >> 1) + wn * (TN * 16)
+                             : (int64_t)tc.tn * BN + wn * (TN * 32);
+    EpiParamsEarly<TM, TN, PAIR, Epi> early;
+    early.load(ep, wm0, wn0, sh.M, PAIR ? sh.N >> 1 : sh.N);
+    wait_vm<0>();
+    early.settle();
+    EpiParams<TM, TN, PAIR, Epi> prm;
+    early.expand(ep, prm);
+    if constexpr (PAIR) {
+      epilogue_pair<TM, TN>(acc, wm0, wn0, sh.M, sh.N >> 1, ep, strip, prm);
+    } else {
+      epilogue_single<TM, TN>(acc, wm0, wn0, sh.M, sh.N, ep, strip, prm);
+    }
+  }
   wait_vm<0>();    // zero-fill copies past the last tile still target the ring
 }
 

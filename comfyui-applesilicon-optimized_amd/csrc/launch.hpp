@@ -95,9 +95,37 @@ inline bool pingpong_on() {
   return Op::kPingPong;
 }
 
+// K from which fp8 GEMMs on the 256x256 tile take gemm_w4_kernel
+// (MI355X, same-process A/B against the 8-wave kernel, bits identical:
+// 16384 rows, K = 13824 +11.6 %, K = 8192 +3.6 %, K = 5120 0 to +3 %,
+// K = 3072 -3 to -5 %).
+constexpr int64_t kW4MinK = 5120;
+
+template <class Op> struct IsF8 : std::false_type {};
+template <int KS> struct IsF8<OpF8T<KS>> : std::true_type {};
+
+// fp8 on the 256x256 tile: gemm_w4_kernel (one wave per SIMD, 128-K stages)
+// where K is long. C4Q_W4=0 / 1 in the environment forces either, for
+// sweeps.
+inline bool w4_for_fp8(int64_t K) {
+  const char* e = getenv("C4Q_W4");
+  if (e && (e[0] == '0' || e[0] == '1') && e[1] == 0) return e[0] == '1';
+  return K >= kW4MinK;
+}
+
 template <class T, class Op, bool PAIR, class Epi>
 int launch_tile(const GemmShape& sh, const Src2& sa, const Src2& sb, const float* b_scale,
                 const Epi& epi, hipStream_t s, const char* what) {
+  if constexpr (IsF8<Op>::value && !PAIR && T::BM == 256 && T::BN == 256 && T::WM == 2 &&
+                T::WN == 4 && T::KG == 1) {
+    if (w4_for_fp8(sh.K)) {
+      auto kernel = gemm_w4_kernel<OpF8T<128>, 2, false, Epi>;
+      static int wocc = 0;
+      const int grid = persistent_grid(kernel, 256, sh.count, wocc);
+      hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(256), 0, s, sh, sa, sb, b_scale, epi);
+      return check_launch(what);
+    }
+  }
   if constexpr (T::WM == 2 && T::WN == 4) {
     using POp = typename PingPongOp<Op>::type;
     constexpr int pbuf = ring_depth<T, POp, PAIR>();

@@ -632,6 +632,63 @@ def test_scaled_mm_pertensor_vs_torch_cpu(dev):
     assert_close(bf16_to_f32(bits16(out)), ref.float().numpy(), "scaled_mm vs torch CPU")
 
 
+# fp8 GEMMs whose plan takes the 256x256 tile run the one-wave-per-SIMD
+# kernel when K >= 5120 (C4Q_W4 forces either kernel; C4Q_TILE=0 forces the
+# 256x256 tile for small shapes). Each output takes its K steps in the same
+# order on both kernels: bits equal, and close to the oracle. Cases: whole
+# tiles; ragged M and N with K % 128 = 80 and 16 (zero-filled K tail);
+# vector and per-tensor scales; bias; bf16, f16 and f32 outputs; several
+# tiles per workgroup (M x N beyond one round).
+W4_CASES = [
+    (512, 5120, 768, "tensor", torch.bfloat16, False, True),
+    (700, 5200, 900, "vector", torch.bfloat16, True, True),
+    (300, 6160, 260, "vector", torch.float32, True, True),
+    (256, 1024, 512, "tensor", torch.float16, False, True),
+    (1000, 2048, 1100, "vector", torch.bfloat16, True, True),
+    (4352, 640, 4480, "tensor", torch.bfloat16, True, True),
+]
+
+
+@pytest.mark.parametrize("M,K,N,scales,out_dtype,with_bias,force_tile", W4_CASES)
+def test_scaled_mm_one_wave_kernel(dev, monkeypatch, M, K, N, scales, out_dtype, with_bias,
+                                   force_tile):
+    g = gen(3 * M + K + N)
+    a = _fp8(torch.randn(M, K, generator=g) * 0.3)
+    w = _fp8(torch.randn(N, K, generator=g) * 0.3)
+    if scales == "vector":
+        sa, sb = torch.rand(M, 1, generator=g) + 0.5, torch.rand(1, N, generator=g) + 0.5
+    else:
+        sa, sb = torch.tensor(0.7), torch.tensor(1.3)
+    bias = torch.randn(N, generator=g) if with_bias else None
+    if force_tile:
+        monkeypatch.setenv("C4Q_TILE", "0")
+    ad, wd = a.to(dev), w.to(dev)
+
+    def run(route):
+        monkeypatch.setenv("C4Q_W4", route)
+        out = ops.scaled_mm(ad, wd.t(), out_dtype=out_dtype, scale_a=sa.to(dev), scale_b=sb.to(dev),
+                            bias=None if bias is None else bias.to(dev))
+        return out.cpu()
+
+    one_wave, eight_wave = run("1"), run("0")
+    od = {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "f32"}[out_dtype]
+    if od == "f32":
+        assert np.array_equal(one_wave.numpy().view(np.uint32), eight_wave.numpy().view(np.uint32)), \
+            f"one-wave vs 8-wave {M}x{K}x{N}"
+        got = one_wave.numpy()
+    else:
+        assert_bits_equal(bits16(one_wave), bits16(eight_wave), f"one-wave vs 8-wave {M}x{K}x{N}")
+        got = (bf16_to_f32 if od == "bf16" else f16_bits_to_f32)(bits16(one_wave))
+    ref = of.scaled_mm(u8(a), u8(w), sa.numpy(), sb.numpy(),
+                       None if bias is None else bias.numpy(), "f32", None, od)
+    if od == "bf16":
+        ref = bf16_to_f32(ref)
+    elif od == "f16":
+        ref = f16_bits_to_f32(ref)
+    tol = {} if od != "f32" else dict(maxabs_rel=2.0 ** -14, rel_l2=2.0 ** -16)
+    assert_close(got, ref, f"one-wave scaled_mm {M}x{K}x{N}", **tol)
+
+
 # ---------------------------------------------------------------- W8A16 ---
 
 @pytest.mark.parametrize("M,K,N,xdt,scaled,bias_dt", [
