@@ -17,6 +17,12 @@
 //                              accumulators v[0..3] and the row / column
 //                              parameters; pair epilogues: apply(r, c, g, u)
 //                              from gate / up sums
+//   kVariants, variant(),      the optional terms present (a bias, a result
+//   apply<V>(...)              scale, activation tables) as a bit mask V
+//                              fixed per call: apply<V> has no per-element
+//                              test of them; apply(...) dispatches on
+//                              variant() (the tiled kernels select V once
+//                              per tile, see with_variant)
 //   value4(m, n, v, nv)        = apply(rowp(m), col(n, nv), v)
 //   row(m), vec                byte pointer to output row m; rows are
 //                              16-byte aligned (chunked stores allowed)
@@ -139,6 +145,9 @@ struct EpiI32 : EpiOut<uint32_t> {
   __device__ __forceinline__ uint32_t col_raw(int, int64_t, int64_t) const { return 0; }
   __device__ __forceinline__ float col_val(int, uint32_t) const { return 0.0f; }
   __device__ __forceinline__ uint32_t row_raw(int64_t, int64_t) const { return 0; }
+  static constexpr int kVariants = 1;
+  __device__ __forceinline__ int variant() const { return 0; }
+  template <int V = 0>
   __device__ __forceinline__ uint4 apply(float, const Col&, const int32_t (&v)[4]) const {
     return uint4{(uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]};
   }
@@ -165,12 +174,18 @@ struct EpiRowScale : EpiOut<uint16_t> {
   __device__ __forceinline__ uint32_t col_raw(int, int64_t n, int64_t N) const { return raw_load16(bias, N, n); }
   __device__ __forceinline__ float col_val(int, uint32_t w) const { return bias ? bf16_f32((uint16_t)w) : 0.0f; }
   __device__ __forceinline__ uint32_t row_raw(int64_t m, int64_t M) const { return raw_load32(rs, M, m); }
+  static constexpr int kVariants = 2;                       // bit 0: bias
+  __device__ __forceinline__ int variant() const { return bias ? 1 : 0; }
+  template <int V>
   __device__ __forceinline__ uint2 apply(float r, const Col& c, const int32_t (&v)[4]) const {
     uint2 p = pack_bf16x4<uint2>((float)v[0] * r, (float)v[1] * r, (float)v[2] * r, (float)v[3] * r);
-    if (bias)
+    if constexpr ((V & 1) != 0)
       p = pack_bf16x4<uint2>(bf16lo(p.x) + c.b[0], bf16hi(p.x) + c.b[1], bf16lo(p.y) + c.b[2],
                              bf16hi(p.y) + c.b[3]);
     return p;
+  }
+  __device__ __forceinline__ uint2 apply(float r, const Col& c, const int32_t (&v)[4]) const {
+    return bias ? apply<1>(r, c, v) : apply<0>(r, c, v);
   }
   __device__ __forceinline__ uint2 value4(int64_t m, int64_t n, const int32_t (&v)[4], int nv) const {
     return apply(rowp(m), col(n, nv), v);
@@ -210,15 +225,21 @@ struct EpiRowColScaleT : EpiOut<uint16_t> {
     if constexpr (F16) return uint2{f16x2_rne(a, b), f16x2_rne(c, d)};
     return pack_bf16x4<uint2>(a, b, c, d);
   }
+  static constexpr int kVariants = 2;                       // bit 0: bias
+  __device__ __forceinline__ int variant() const { return bias ? 1 : 0; }
+  template <int V>
   __device__ __forceinline__ uint2 apply(float r, const Col& c, const int32_t (&v)[4]) const {
     float x[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) x[q] = (float)v[q] * (c.s[q] * r);
     uint2 p = pack(x[0], x[1], x[2], x[3]);
-    if (bias)
+    if constexpr ((V & 1) != 0)
       p = pack(out_f32((uint16_t)p.x) + c.b[0], out_f32((uint16_t)(p.x >> 16)) + c.b[1],
                out_f32((uint16_t)p.y) + c.b[2], out_f32((uint16_t)(p.y >> 16)) + c.b[3]);
     return p;
+  }
+  __device__ __forceinline__ uint2 apply(float r, const Col& c, const int32_t (&v)[4]) const {
+    return bias ? apply<1>(r, c, v) : apply<0>(r, c, v);
   }
   __device__ __forceinline__ uint2 value4(int64_t m, int64_t n, const int32_t (&v)[4], int nv) const {
     return apply(rowp(m), col(n, nv), v);
@@ -331,14 +352,15 @@ struct EpiQKVNormRope : EpiRowColScaleQKV {
 // torch._scaled_mm on the fp8 route: out = f32 acc, then * scale_a,
 // * scale_b, * scale_result, + f32(bias), each in f32 and in this order,
 // one final rounding to the output dtype
-// (reference _patches/scaled_mm_fp8.py:123-146). F32OUT selects a 32-bit
-// output; otherwise out_dt picks bf16 or f16. Scale pointers are read with a
-// stride (0: per tensor, 1: per row / column); an absent scale reads 1.0f.
-template <bool F32OUT>
-struct EpiScaled : EpiOut<typename std::conditional<F32OUT, uint32_t, uint16_t>::type> {
-  using Base = EpiOut<typename std::conditional<F32OUT, uint32_t, uint16_t>::type>;
+// (reference _patches/scaled_mm_fp8.py:123-146). OUT is the output type
+// (DT_BF16, DT_F16 or DT_F32), fixed at compile time so that the store loop
+// converts one way. Scale pointers are read with a stride (0: per tensor, 1:
+// per row / column); an absent scale reads 1.0f, an absent scale_result is
+// skipped (x * 1.0f == x).
+template <int OUT>
+struct EpiScaled : EpiOut<typename std::conditional<OUT == DT_F32, uint32_t, uint16_t>::type> {
+  using Base = EpiOut<typename std::conditional<OUT == DT_F32, uint32_t, uint16_t>::type>;
   using Packed = typename Base::Packed;
-  int out_dt;
   const float* sa; int sa_mode; const float* sb; int sb_mode; const float* sr;
   const void* bias; int bias_dt;
   int sa_step, sb_step;
@@ -375,19 +397,35 @@ struct EpiScaled : EpiOut<typename std::conditional<F32OUT, uint32_t, uint16_t>:
   __device__ __forceinline__ uint32_t row_raw(int64_t m, int64_t M) const {
     return raw_load32(sa, sa_step ? M : 1, m * sa_step);
   }
+  static constexpr int kVariants = 4;                       // bit 0: bias, bit 1: scale_result
+  __device__ __forceinline__ int variant() const { return (bias ? 1 : 0) | (sr ? 2 : 0); }
+  template <int V>
   __device__ __forceinline__ Packed apply(float a, const Col& c, const float (&v)[4]) const {
     float o[4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) o[q] = ((v[q] * a) * c.s[q]) * sr0;
-    if (bias) {
+    for (int q = 0; q < 4; ++q) o[q] = (v[q] * a) * c.s[q];
+    if constexpr ((V & 2) != 0) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) o[q] = o[q] * sr0;
+    }
+    if constexpr ((V & 1) != 0) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) o[q] = o[q] + c.b[q];
     }
-    if constexpr (F32OUT) {
+    if constexpr (OUT == DT_F32) {
       return Packed{f32_bits(o[0]), f32_bits(o[1]), f32_bits(o[2]), f32_bits(o[3])};
+    } else if constexpr (OUT == DT_F16) {
+      return Packed{f16x2_rne(o[0], o[1]), f16x2_rne(o[2], o[3])};
     } else {
-      if (out_dt == DT_F16) return Packed{f16x2_rne(o[0], o[1]), f16x2_rne(o[2], o[3])};
       return pack_bf16x4<Packed>(o[0], o[1], o[2], o[3]);
+    }
+  }
+  __device__ __forceinline__ Packed apply(float a, const Col& c, const float (&v)[4]) const {
+    switch (variant()) {
+      case 1: return apply<1>(a, c, v);
+      case 2: return apply<2>(a, c, v);
+      case 3: return apply<3>(a, c, v);
+      default: return apply<0>(a, c, v);
     }
   }
   __device__ __forceinline__ Packed value4(int64_t m, int64_t n, const float (&v)[4], int nv) const {
@@ -399,12 +437,13 @@ struct EpiScaled : EpiOut<typename std::conditional<F32OUT, uint32_t, uint16_t>:
 // _patches/fp8s_ext/w8a16_gemm.mm:101-119 and the f32-out + bias route of
 // _patches/linear_fp8_w8a16.py:190-196). `act` (bf16 output only) is a
 // 65,536-entry table applied to the rounded bf16 value: the unfused
-// "bf16 linear, then bf16 activation" order of the FLUX MLP.
-template <bool F32OUT>
-struct EpiW8A16 : EpiOut<typename std::conditional<F32OUT, uint32_t, uint16_t>::type> {
-  using Base = EpiOut<typename std::conditional<F32OUT, uint32_t, uint16_t>::type>;
+// "bf16 linear, then bf16 activation" order of the FLUX MLP. OUT is the
+// output type (DT_BF16, DT_F16 or DT_F32), fixed at compile time.
+template <int OUT>
+struct EpiW8A16 : EpiOut<typename std::conditional<OUT == DT_F32, uint32_t, uint16_t>::type> {
+  using Base = EpiOut<typename std::conditional<OUT == DT_F32, uint32_t, uint16_t>::type>;
   using Packed = typename Base::Packed;
-  int out_dt; const void* bias; int bias_dt; const uint16_t* act;
+  const void* bias; int bias_dt; const uint16_t* act;
   struct Col { float b[4]; };
   __device__ __forceinline__ EpiW8A16 prepare() const { return *this; }
   __device__ __forceinline__ Col col(int64_t n, int nv) const {
@@ -420,22 +459,36 @@ struct EpiW8A16 : EpiOut<typename std::conditional<F32OUT, uint32_t, uint16_t>::
   }
   __device__ __forceinline__ float col_val(int, uint32_t w) const { return bias ? raw_f32(w, bias_dt) : 0.0f; }
   __device__ __forceinline__ uint32_t row_raw(int64_t, int64_t) const { return 0; }
+  static constexpr int kVariants = OUT == DT_BF16 ? 4 : 2;   // bit 0: bias, bit 1: act
+  __device__ __forceinline__ int variant() const {
+    return (bias ? 1 : 0) | (OUT == DT_BF16 && act ? 2 : 0);
+  }
+  template <int V>
   __device__ __forceinline__ Packed apply(float, const Col& c, const float (&v)[4]) const {
     float o[4] = {v[0], v[1], v[2], v[3]};
-    if (bias) {
+    if constexpr ((V & 1) != 0) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) o[q] = o[q] + c.b[q];
     }
-    if constexpr (F32OUT) {
+    if constexpr (OUT == DT_F32) {
       return Packed{f32_bits(o[0]), f32_bits(o[1]), f32_bits(o[2]), f32_bits(o[3])};
+    } else if constexpr (OUT == DT_F16) {
+      return Packed{f16x2_rne(o[0], o[1]), f16x2_rne(o[2], o[3])};
     } else {
-      if (out_dt == DT_F16) return Packed{f16x2_rne(o[0], o[1]), f16x2_rne(o[2], o[3])};
       Packed p = pack_bf16x4<Packed>(o[0], o[1], o[2], o[3]);
-      if (act) {
+      if constexpr ((V & 2) != 0) {
         p.x = (uint32_t)act[p.x & 0xFFFFu] | ((uint32_t)act[p.x >> 16] << 16);
         p.y = (uint32_t)act[p.y & 0xFFFFu] | ((uint32_t)act[p.y >> 16] << 16);
       }
       return p;
+    }
+  }
+  __device__ __forceinline__ Packed apply(float r, const Col& c, const float (&v)[4]) const {
+    switch (variant()) {
+      case 1: return apply<1>(r, c, v);
+      case 2: return apply<2 % kVariants>(r, c, v);
+      case 3: return apply<3 % kVariants>(r, c, v);
+      default: return apply<0>(r, c, v);
     }
   }
   __device__ __forceinline__ Packed value4(int64_t m, int64_t n, const float (&v)[4], int nv) const {
@@ -471,6 +524,9 @@ struct EpiPair : EpiOut<uint16_t> {
   }
   __device__ __forceinline__ float col_val(int, uint32_t w) const { return bits_f32(w); }
   __device__ __forceinline__ uint32_t row_raw(int64_t m, int64_t M) const { return raw_load32(rs, M, m); }
+  static constexpr int kVariants = 4;                       // bit 0: t1, bit 1: t2
+  __device__ __forceinline__ int variant() const { return (t1 ? 1 : 0) | (t2 ? 2 : 0); }
+  template <int V>
   __device__ __forceinline__ uint2 apply(float r, const Col& c, const int32_t (&g)[4],
                                          const int32_t (&u)[4]) const {
     float a[4], b[4];
@@ -481,16 +537,25 @@ struct EpiPair : EpiOut<uint16_t> {
     }
     uint2 x1 = pack_bf16x4<uint2>(a[0], a[1], a[2], a[3]);
     uint2 x2 = pack_bf16x4<uint2>(b[0], b[1], b[2], b[3]);
-    if (t1) {
+    if constexpr ((V & 1) != 0) {
       x1.x = (uint32_t)t1[x1.x & 0xFFFFu] | ((uint32_t)t1[x1.x >> 16] << 16);
       x1.y = (uint32_t)t1[x1.y & 0xFFFFu] | ((uint32_t)t1[x1.y >> 16] << 16);
     }
-    if (t2) {
+    if constexpr ((V & 2) != 0) {
       x2.x = (uint32_t)t2[x2.x & 0xFFFFu] | ((uint32_t)t2[x2.x >> 16] << 16);
       x2.y = (uint32_t)t2[x2.y & 0xFFFFu] | ((uint32_t)t2[x2.y >> 16] << 16);
     }
     return pack_bf16x4<uint2>(bf16lo(x1.x) * bf16lo(x2.x), bf16hi(x1.x) * bf16hi(x2.x),
                               bf16lo(x1.y) * bf16lo(x2.y), bf16hi(x1.y) * bf16hi(x2.y));
+  }
+  template <class T>
+  __device__ __forceinline__ uint2 apply(float r, const Col& c, const T (&g)[4], const T (&u)[4]) const {
+    switch (variant()) {
+      case 1: return apply<1>(r, c, g, u);
+      case 2: return apply<2>(r, c, g, u);
+      case 3: return apply<3>(r, c, g, u);
+      default: return apply<0>(r, c, g, u);
+    }
   }
   __device__ __forceinline__ uint2 pair4(int64_t m, int64_t n, const int32_t (&g)[4],
                                          const int32_t (&u)[4], int nv) const {
@@ -512,20 +577,32 @@ struct EpiPairF : EpiOut<uint16_t> {
   __device__ __forceinline__ uint32_t col_raw(int, int64_t, int64_t) const { return 0; }
   __device__ __forceinline__ float col_val(int, uint32_t) const { return 0.0f; }
   __device__ __forceinline__ uint32_t row_raw(int64_t, int64_t) const { return 0; }
+  static constexpr int kVariants = 4;                       // bit 0: t1, bit 1: t2
+  __device__ __forceinline__ int variant() const { return (t1 ? 1 : 0) | (t2 ? 2 : 0); }
+  template <int V>
   __device__ __forceinline__ uint2 apply(float, const Col&, const float (&g)[4],
                                          const float (&u)[4]) const {
     uint2 x1 = pack_bf16x4<uint2>(g[0], g[1], g[2], g[3]);
     uint2 x2 = pack_bf16x4<uint2>(u[0], u[1], u[2], u[3]);
-    if (t1) {
+    if constexpr ((V & 1) != 0) {
       x1.x = (uint32_t)t1[x1.x & 0xFFFFu] | ((uint32_t)t1[x1.x >> 16] << 16);
       x1.y = (uint32_t)t1[x1.y & 0xFFFFu] | ((uint32_t)t1[x1.y >> 16] << 16);
     }
-    if (t2) {
+    if constexpr ((V & 2) != 0) {
       x2.x = (uint32_t)t2[x2.x & 0xFFFFu] | ((uint32_t)t2[x2.x >> 16] << 16);
       x2.y = (uint32_t)t2[x2.y & 0xFFFFu] | ((uint32_t)t2[x2.y >> 16] << 16);
     }
     return pack_bf16x4<uint2>(bf16lo(x1.x) * bf16lo(x2.x), bf16hi(x1.x) * bf16hi(x2.x),
                               bf16lo(x1.y) * bf16lo(x2.y), bf16hi(x1.y) * bf16hi(x2.y));
+  }
+  template <class T>
+  __device__ __forceinline__ uint2 apply(float r, const Col& c, const T (&g)[4], const T (&u)[4]) const {
+    switch (variant()) {
+      case 1: return apply<1>(r, c, g, u);
+      case 2: return apply<2>(r, c, g, u);
+      case 3: return apply<3>(r, c, g, u);
+      default: return apply<0>(r, c, g, u);
+    }
   }
   __device__ __forceinline__ uint2 pair4(int64_t m, int64_t n, const float (&g)[4],
                                          const float (&u)[4], int nv) const {

@@ -39,14 +39,15 @@ extern "C" int c4q_f8_gemm_nt_scaled(const uint8_t* a, int64_t lda, const uint8_
   C4Q_REQUIRE(!bias || valid_dt(bias_dtype), C4Q_ERR_ARG, "%s: bad bias dtype", what);
   if (M == 0 || N == 0) return C4Q_OK;
   C4Q_REQUIRE(d && (K == 0 || (a && b)), C4Q_ERR_ARG, "%s: null pointer", what);
-  if (d_dtype == C4Q_F32) {
-    EpiScaled<true> epi{{d, ldd, rows_vec16(d, ldd, 4)}, d_dtype, scale_a, scale_a_mode, scale_b,
-                        scale_b_mode, scale_result, bias, bias_dtype, 0, 0, 1.0f};
+  auto run = [&](auto out) {
+    constexpr int OUT = decltype(out)::value;
+    EpiScaled<OUT> epi{{d, ldd, rows_vec16(d, ldd, OUT == DT_F32 ? 4 : 2)}, scale_a, scale_a_mode,
+                       scale_b, scale_b_mode, scale_result, bias, bias_dtype, 0, 0, 1.0f};
     return run_gemm8<OpF8Any, GenF8>(a, lda, b, ldb, M, N, K, epi, as_stream(stream), what);
-  }
-  EpiScaled<false> epi{{d, ldd, rows_vec16(d, ldd, 2)}, d_dtype, scale_a, scale_a_mode, scale_b,
-                       scale_b_mode, scale_result, bias, bias_dtype, 0, 0, 1.0f};
-  return run_gemm8<OpF8Any, GenF8>(a, lda, b, ldb, M, N, K, epi, as_stream(stream), what);
+  };
+  if (d_dtype == C4Q_F32) return run(std::integral_constant<int, DT_F32>{});
+  if (d_dtype == C4Q_F16) return run(std::integral_constant<int, DT_F16>{});
+  return run(std::integral_constant<int, DT_BF16>{});
 }
 
 namespace {
@@ -155,10 +156,13 @@ extern "C" int c4q_w8a16_gemm_nt(const void* a, int a_dtype, int64_t lda, const 
   if (M == 0 || N == 0) return C4Q_OK;
   C4Q_REQUIRE(d && (K == 0 || (a && w)), C4Q_ERR_ARG, "%s: null pointer", what);
   hipStream_t s = as_stream(stream);
-  if (d_dtype == C4Q_F32) {
-    EpiW8A16<true> epi{{d, ldd, rows_vec16(d, ldd, 4)}, d_dtype, bias, bias_dtype, act_table};
+  auto run = [&](auto out) {
+    constexpr int OUT = decltype(out)::value;
+    EpiW8A16<OUT> epi{{d, ldd, rows_vec16(d, ldd, OUT == DT_F32 ? 4 : 2)}, bias, bias_dtype,
+                      act_table};
     return run_w8a16(a, a_dtype, lda, w, ldw, w_scale, M, N, K, epi, s, what);
-  }
-  EpiW8A16<false> epi{{d, ldd, rows_vec16(d, ldd, 2)}, d_dtype, bias, bias_dtype, act_table};
-  return run_w8a16(a, a_dtype, lda, w, ldw, w_scale, M, N, K, epi, s, what);
+  };
+  if (d_dtype == C4Q_F32) return run(std::integral_constant<int, DT_F32>{});
+  if (d_dtype == C4Q_F16) return run(std::integral_constant<int, DT_F16>{});
+  return run(std::integral_constant<int, DT_BF16>{});
 }
