@@ -391,6 +391,16 @@ struct OpW8A16 {
       for (int i = 0; i < TM; ++i) acc[i][j] = mfma(f.a[1][i], b1, acc[i][j]);
     }
   }
+  // Word W (0..3) of a raw 16-code chunk dequantized into its two MFMA
+  // operands (word W feeds K half W / 2), for schedules that interleave the
+  // dequant with MFMAs one word at a time (gemm_w4a16_kernel).
+  template <int W>
+  __device__ __forceinline__ static void dequant_word(const i32x4& q, float ws, i32x4 (&b)[2]) {
+    uint32_t lo, hi;
+    dequant4<BF16, HAS_SCALE>((uint32_t)q[W], ws, lo, hi);
+    b[W / 2][2 * (W % 2)] = (int)lo;
+    b[W / 2][2 * (W % 2) + 1] = (int)hi;
+  }
 };
 
 // bf16 x bf16 -> fp32, v_mfma_f32_32x32x16_bf16 (the MOSS bf16 FFN pair):
@@ -1471,6 +1481,219 @@ gemm_w4_kernel(GemmShape sh, Src2 sa, Src2 sb, const float* b_scale, Epi epi) {
     } else {
       epilogue_single<TM, TN>(acc, wm0, wn0, sh.M, sh.N, ep, strip, prm);
     }
+  }
+  wait_vm<0>();    // zero-fill copies past the last tile still target the ring
+}
+
+// W8A16 with one wave per SIMD: a 256 x 256 tile of four waves, each a
+// TM x TN grid of 32x32 blocks (WM x WN = 1 x 4: 256 x 64 per wave, each
+// dequantized weight block feeds 8 MFMAs; 2 x 2: 128 x 128, 4 MFMAs),
+// bf16/f16 activations and fp8 weights through a three-stage ring of 64-K
+// stages (48 KB each). Against the 8-wave ping-pong tile the waves meet at
+// one barrier per stage instead of two, and with 1 x 4 they dequantize
+// each weight element once per tile row instead of twice.
+//
+// A K step (32 K values) is a stream of 2 TM TN MFMA slots, blocks in
+// column order: slot k = (j, h, i) multiplies A block i (K half h) with
+// weight block j. The fragments and dequantized weights of the next step
+// are produced under this step's MFMAs, each right after the slot that
+// frees its registers:
+//   * raw fp8 chunk q[j] of the next step is read at the first slot of
+//     block j's column for j < TN - 1 (its previous contents were
+//     dequantized in the previous step) and of block 1 for j = TN - 1;
+//   * q[j] (j < TN - 1) is dequantized into the operands b[j][.] during the
+//     slots of column j + 1, after the last MFMA that reads b[j][.]; q[TN-1]
+//     during column 0 of the step it belongs to (its operands are first
+//     read in the last column);
+//   * A fragment (h, i) is read after its last reader in the last column;
+//   * in a stage's last step, after the stage barrier, the wave's 12
+//     copies of stage gs + NBUF go out one every other slot.
+// LDS reads use per-lane offsets computed once (the swizzled chunk of a
+// lane is the same for every block row), plus the stage base, plus a
+// constant block offset in the instruction. Reads of the next step come
+// from the current stage buffer (first step) or, after the barrier, from
+// the next one (last step); across tiles the ring already holds the next
+// tile's first stage. Each accumulator takes its K steps and K halves in
+// the order of gemm_pingpong_kernel, so the results are the same bits.
+template <bool BF16, bool HAS_SCALE, int WM, int WN, int NBUF, class Epi>
+__global__ void __launch_bounds__(256)
+gemm_w4a16_kernel(GemmShape sh, Src2 sa, Src2 sb, const float* b_scale, Epi epi) {
+  using Op = OpW8A16<BF16, HAS_SCALE>;
+  constexpr int BM = 256, BN = 256, NT = 256;
+  static_assert(WM * WN == 4, "four waves");
+  constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
+  static_assert(TN >= 2 && TM >= 4, "the slot schedule needs two block columns and four rows");
+  constexpr int SA = Op::SA, SB = Op::SB, S = Op::S;
+  static_assert(S == 2, "two K steps per stage");
+  constexpr int STAGE = BM * SA + BN * SB;
+  constexpr int RING = NBUF * STAGE;
+  constexpr int kStrip = strip_bytes<TN, false>();
+  static_assert(NBUF >= 3 && RING + kStrip * WM * WN <= 160 * 1024, "LDS exceeds 160 KB");
+  using LA = DirectLoad<BM, SA, NT, false>;
+  using LB = DirectLoad<BN, SB, NT, false>;
+  constexpr int kPerStage = LA::kInstr + LB::kInstr;     // copies per wave per stage
+  constexpr int kSlots = 2 * TM * TN, kCol = 2 * TM;      // MFMA slots per step / per column
+  static_assert(2 * kPerStage <= kSlots, "one copy every other slot");
+  static_assert((NBUF - 1) * kPerStage < 64, "too many copies in flight for vmcnt");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[RING + kStrip * WM * WN];
+
+  const int ntiles = sh.count;
+  const int G = (int)gridDim.x;
+  const int my_tiles = (ntiles - 1 - (int)blockIdx.x) / G + 1;
+  const Epi ep = epi.prepare();
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform
+  const int wm = wave / WN, wn = wave % WN;
+  const float ws = Op::prep_scale(b_scale);
+
+  LA la;
+  LB lb;
+  la.init(sa.ld_bytes, wave, 0);
+  lb.init(sb.ld_bytes, wave, 0);
+  constexpr int KS = Op::kStageK;
+  const int a_kb = (int)(sh.K * SA / KS), b_kb = (int)(sh.K * SB / KS);
+  const int nst = (int)((sh.K + KS - 1) / KS);
+
+  int ij = 0, ips = 0;
+  u32x4 ra, rb0;
+  auto tile_rsrc = [&](int j) __attribute__((always_inline)) {
+    const TileCoord tc = tile_at(sh, (int)blockIdx.x + j * G);
+    const int64_t m0 = (int64_t)tc.tm * BM;
+    const int64_t brow0 = (int64_t)tc.tn * BN;
+    ra = dma_rsrc(sa.p0 + m0 * sa.ld_bytes, (sa.rows - m0) * sa.ld_bytes);
+    rb0 = dma_rsrc(sb.p0 + brow0 * sb.ld_bytes, (sb.rows - brow0) * sb.ld_bytes);
+  };
+  // Copy C of the next stage (A copies first) into `buf`; past this
+  // workgroup's last tile the copies read zeros, so every stage issues the
+  // same number of copies and the vmcnt arithmetic stays fixed.
+  auto issue_copy = [&](auto cc, uint8_t* buf, bool live) __attribute__((always_inline)) {
+    constexpr int C = decltype(cc)::value;
+    if constexpr (C < LA::kInstr) {
+      la.template issue_one<C>(ra, ra, buf, live ? ips * SA : 0, live ? a_kb : 0);
+    } else {
+      lb.template issue_one<C - LA::kInstr>(rb0, rb0, buf + BM * SA, live ? ips * SB : 0,
+                                            live ? b_kb : 0);
+    }
+  };
+  auto advance = [&]() __attribute__((always_inline)) {
+    if (ij < my_tiles && ++ips == nst) {
+      ips = 0;
+      if (++ij < my_tiles) tile_rsrc(ij);
+    }
+  };
+  tile_rsrc(0);
+
+  // prologue: stages 0 .. NBUF-1 in flight, stage 0 complete and visible
+#pragma unroll
+  for (int p = 0; p < NBUF; ++p) {
+    const bool live = ij < my_tiles;
+    static_for<0, kPerStage>([&](auto cc) { issue_copy(cc, smem + p * STAGE, live); });
+    advance();
+  }
+  wait_vm<(NBUF - 1) * kPerStage>();
+  stage_barrier();
+
+  // Per-lane LDS byte offsets within a stage: A fragment of K step t, half
+  // H, block row 0 (block row i adds 32 i rows), and the raw weight chunk of
+  // K step t, block column 0 (column j adds 32 j rows). The swizzle of a row
+  // depends on its low 4 bits only, so the chunk a lane reads is the same
+  // for every block.
+  const int lane = threadIdx.x & 63, lr = lane & 31, hl = lane >> 5;
+  const int ra0 = wm * (TM * 32), rb0i = wn * (TN * 32);
+  uint32_t offa[2][2], offb[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+      offa[t][hh] = (uint32_t)((ra0 + lr) * SA + phys_chunk<SA>(ra0 + lr, 4 * t + 2 * hl + hh) * 16);
+    offb[t] = (uint32_t)(BM * SA + (rb0i + lr) * SB + phys_chunk<SB>(rb0i + lr, 2 * t + hl) * 16);
+  }
+  typedef __attribute__((address_space(3))) const i32x4 lds_i32x4;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const uint8_t*)smem;
+  i32x4 fa[2][TM];        // A fragments of the current step: [K half][block row]
+  i32x4 fq[TN];           // raw fp8 chunks (next step's, once read)
+  i32x4 bq[TN][2];        // dequantized weight operands: [block column][K half]
+  // step 0 of the first tile: A and all raw chunks; columns 0 .. TN-2
+  // dequantized now, the last one in the first step's column 0
+  static_for<0, 2>([&](auto hc) {
+    constexpr int hh = decltype(hc)::value;
+    static_for<0, TM>([&](auto ic) {
+      constexpr int i = decltype(ic)::value;
+      fa[hh][i] = reinterpret_cast<lds_i32x4*>(lds0 + offa[0][hh])[i * 32 * SA / 16];
+    });
+  });
+  static_for<0, TN>([&](auto jc) {
+    constexpr int j = decltype(jc)::value;
+    fq[j] = reinterpret_cast<lds_i32x4*>(lds0 + offb[0])[j * 32 * SB / 16];
+  });
+  static_for<0, TN - 1>([&](auto jc) {
+    constexpr int j = decltype(jc)::value;
+    static_for<0, 4>([&](auto wc) { Op::template dequant_word<decltype(wc)::value>(fq[j], ws, bq[j]); });
+  });
+  uint8_t* strip = smem + RING + wave * kStrip;
+  int gs = 0;                                   // stage counter over all tiles
+  for (int j = 0; j < my_tiles; ++j) {
+    typename Op::Acc acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int jj = 0; jj < TN; ++jj)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][jj][r] = 0;
+    auto stage = [&]() __attribute__((always_inline)) {
+      const int cb = gs % NBUF, nb = (gs + 1) % NBUF;
+      uint8_t* cur = smem + cb * STAGE;
+      static_for<0, S>([&](auto sc) {
+        constexpr int s = decltype(sc)::value;
+        constexpr bool kLast = s == S - 1;
+        if constexpr (kLast) {
+          wait_vm<(NBUF - 2) * kPerStage>();   // this wave's copies of stage gs + 1 landed
+          stage_barrier_tracked();             // ... and every wave's; stage gs fully read
+        }
+        constexpr int ft = kLast ? 0 : s + 1;  // K step (within its stage) being prefetched
+        const uint32_t sbase = lds0 + (uint32_t)((kLast ? nb : cb) * STAGE);
+        const uint32_t pa0 = sbase + offa[ft][0], pa1 = sbase + offa[ft][1], pb = sbase + offb[ft];
+        const bool live = ij < my_tiles;
+        static_for<0, kSlots>([&](auto kc) {
+          constexpr int k = decltype(kc)::value;
+          constexpr int jb = k / kCol, hh = (k % kCol) / TM, i = k % TM;
+          acc[i][jb] = Op::mfma(fa[hh][i], bq[jb][hh], acc[i][jb]);
+          // raw chunks of the next step
+          if constexpr (k % kCol == 0 && jb < TN - 1)
+            fq[jb] = reinterpret_cast<lds_i32x4*>(pb)[jb * 32 * SB / 16];
+          if constexpr (k == kCol)
+            fq[TN - 1] = reinterpret_cast<lds_i32x4*>(pb)[(TN - 1) * 32 * SB / 16];
+          // dequant: the last column of this step during column 0, column
+          // jb - 1 of the next step during column jb; one word per kCol / 4 slots
+          constexpr int kW = kCol / 4;
+          if constexpr (k % kW == kW - 1) {
+            constexpr int w = (k % kCol) / kW;
+            if constexpr (jb == 0) Op::template dequant_word<w>(fq[TN - 1], ws, bq[TN - 1]);
+            else Op::template dequant_word<w>(fq[jb - 1], ws, bq[jb - 1]);
+          }
+          // A fragments of the next step, after their last reader
+          if constexpr (jb == TN - 1)
+            fa[hh][i] = reinterpret_cast<lds_i32x4*>(hh ? pa1 : pa0)[i * 32 * SA / 16];
+          if constexpr (kLast && k < 2 * kPerStage && k % 2 == 1)
+            issue_copy(std::integral_constant<int, k / 2>{}, cur, live);
+          __builtin_amdgcn_sched_barrier(0);
+        });
+        if constexpr (kLast) advance();
+      });
+      ++gs;
+    };
+    for (int st = 0; st < nst; ++st) stage();
+    // epilogue parameters: issued, then waited for with this wave's copies
+    // in flight (one drain per tile)
+    const TileCoord tc = tile_at(sh, (int)blockIdx.x + j * G);
+    const int64_t wm0 = (int64_t)tc.tm * BM + wm * (TM * 32);
+    const int64_t wn0 = (int64_t)tc.tn * BN + wn * (TN * 32);
+    EpiParamsEarly<TM, TN, false, Epi> early;
+    early.load(ep, wm0, wn0, sh.M, sh.N);
+    wait_vm<0>();
+    early.settle();
+    EpiParams<TM, TN, false, Epi> prm;
+    early.expand(ep, prm);
+    epilogue_single<TM, TN>(acc, wm0, wn0, sh.M, sh.N, ep, strip, prm);
   }
   wait_vm<0>();    // zero-fill copies past the last tile still target the ring
 }

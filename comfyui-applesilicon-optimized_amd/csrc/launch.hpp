@@ -113,9 +113,35 @@ inline bool w4_for_fp8(int64_t K) {
   return K >= kW4MinK;
 }
 
+template <class Op> struct IsW8A16 : std::false_type {};
+template <bool B, bool S> struct IsW8A16<OpW8A16<B, S>> : std::true_type {
+  static constexpr bool kBF16 = B, kScale = S;
+};
+
+// W8A16 on the 256x256 tile: gemm_w4a16_kernel (one wave per SIMD) with
+// 1 x 4 waves (C4Q_W4A16=1) or 2 x 2 waves (=2), or the 8-wave ping-pong
+// kernel (=0), for sweeps.
+inline int w4a16_mode() {
+  const char* e = getenv("C4Q_W4A16");
+  if (e && e[0] >= '0' && e[0] <= '2' && e[1] == 0) return e[0] - '0';
+  return 1;
+}
+
 template <class T, class Op, bool PAIR, class Epi>
 int launch_tile(const GemmShape& sh, const Src2& sa, const Src2& sb, const float* b_scale,
                 const Epi& epi, hipStream_t s, const char* what) {
+  if constexpr (IsW8A16<Op>::value && !PAIR && T::BM == 256 && T::BN == 256 && T::WM == 2 &&
+                T::WN == 4 && T::KG == 1) {
+    const int mode = w4a16_mode();
+    if (mode != 0) {
+      auto kernel = mode == 1 ? gemm_w4a16_kernel<IsW8A16<Op>::kBF16, IsW8A16<Op>::kScale, 1, 4, 3, Epi>
+                              : gemm_w4a16_kernel<IsW8A16<Op>::kBF16, IsW8A16<Op>::kScale, 2, 2, 3, Epi>;
+      static int aocc = 0;
+      const int grid = persistent_grid(kernel, 256, sh.count, aocc);
+      hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(256), 0, s, sh, sa, sb, b_scale, epi);
+      return check_launch(what);
+    }
+  }
   if constexpr (IsF8<Op>::value && !PAIR && T::BM == 256 && T::BN == 256 && T::WM == 2 &&
                 T::WN == 4 && T::KG == 1) {
     if (w4_for_fp8(sh.K)) {
