@@ -33,6 +33,9 @@ _SIGNATURES = {
                                     _I64, _P],
     "c4q_i8_gemm_nt_fused_cs_qkv_rms_rope": [_P, _I64, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _P,
                                              _P, _I64, _I64, _I64, _I64, ctypes.c_float, _P],
+    "c4q_i8_gemm_nt_fused_cs_qkv_lora_part": [_P, _I64, _P, _I64, _P, _P, _P, _P, _P, _P, _P,
+                                              _I64, _I64, _I64, _I64, _I, ctypes.c_float,
+                                              ctypes.c_float, _P],
     "c4q_i8_quant_rowwise": [_P, _I, _I64, _P, _I64, _P, _I64, _I64, _P],
     "c4q_i8_swiglu_rot_quant": [_P, _I64, _I64, _P, _P, _P, _P],
     "c4q_i8_mlp_bridge_prequant": [_P, _I64, _P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _I64,

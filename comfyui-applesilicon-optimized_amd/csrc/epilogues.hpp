@@ -274,6 +274,45 @@ struct EpiRowColScaleQKV : EpiRowColScaleT<false> {
   }
 };
 
+// H3 runtime-LoRA partition (reference int8_matmul_fused_cs_qk_lora_rms_rope
+// and _v_lora, _patches/int8_ext/int8_gemm.mm:915-1085, host :2211-2330):
+// the QKV scatter of ONE partition (Q, K or V: its H D weight rows, so every
+// column has kind 0 and goes to d), with a bf16 low-rank delta [M, H D]
+// added to each projection value after the bias:
+//   sd = bf16(f32(delta[m, n]) * ls),  ls = f32(bf16(delta_scale))
+//   out = bf16(f32(value) + f32(sd))
+// The tiled epilogue calls elem() on each 4-column group after apply().
+struct EpiQKVLora : EpiRowColScaleQKV {
+  static constexpr bool kElem = true;
+  const uint16_t* delta;    // [M, width] bf16, rows contiguous, 8-byte aligned
+  float ls;
+  __device__ __forceinline__ EpiQKVLora prepare() const { return *this; }
+  // the delta term of the 4-column group at (m, n), nv of its columns live
+  // (width % 4 == 0 and n % 4 == 0: a whole group is one 8-byte load)
+  __device__ __forceinline__ uint2 elem(int64_t m, int64_t n, int nv, uint2 p) const {
+    const uint16_t* src = delta + m * (int64_t)width + n;
+    uint32_t w[2];
+    if (nv >= 4) {
+      const uint2 u = *reinterpret_cast<const uint2*>(src);
+      w[0] = u.x;
+      w[1] = u.y;
+    } else {
+      uint16_t h[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) h[q] = src[q < nv ? q : 0];
+      w[0] = (uint32_t)h[0] | ((uint32_t)h[1] << 16);
+      w[1] = (uint32_t)h[2] | ((uint32_t)h[3] << 16);
+    }
+    const uint32_t sd0 = bf16x2_rne(bf16lo(w[0]) * ls, bf16hi(w[0]) * ls);
+    const uint32_t sd1 = bf16x2_rne(bf16lo(w[1]) * ls, bf16hi(w[1]) * ls);
+    return uint2{bf16x2_rne(bf16lo(p.x) + bf16lo(sd0), bf16hi(p.x) + bf16hi(sd0)),
+                 bf16x2_rne(bf16lo(p.y) + bf16lo(sd1), bf16hi(p.y) + bf16hi(sd1))};
+  }
+  __device__ __forceinline__ uint2 value4(int64_t m, int64_t n, const int32_t (&v)[4], int nv) const {
+    return elem(m, n, nv, apply(rowp(m), col(n, nv), v));
+  }
+};
+
 // bf16 rounding (nearest even) of an f32 value, as f32.
 __device__ __forceinline__ float round_bf16(float v) { return bf16lo(bf16x2_rne(v, v)); }
 

@@ -698,6 +698,12 @@ __device__ __forceinline__ void with_variant(const Epi& epi, F&& f) {
   }
 }
 
+// Epilogues with an element-wise term (E::kElem): elem(m, n, nv, packed)
+// is applied to each 4-column group after apply().
+template <class E, class = void> struct HasElem : std::false_type {};
+template <class E>
+struct HasElem<E, std::void_t<decltype(E::kElem)>> : std::bool_constant<E::kElem> {};
+
 template <int V, int TM, int TN, class Acc, class Epi, class Params>
 __device__ __forceinline__ void epilogue_single_v(const Acc (&acc)[TM][TN], int64_t m0, int64_t n0,
                                                   int64_t M, int64_t N, const Epi& epi, uint8_t* lds,
@@ -734,6 +740,10 @@ __device__ __forceinline__ void epilogue_single_v(const Acc (&acc)[TM][TN], int6
             const Scalar* w = sw + St::word(prow, c + 4 * gg);
             const Scalar v[4] = {w[0], w[1], w[2], w[3]};
             out[gg] = epi.template apply<V>(rp[i][q], col[h * Map::GPU + gg], v);
+            if constexpr (HasElem<Epi>::value) {
+              const int64_t kv = nv - 4 * gg;
+              if (kv > 0) out[gg] = epi.elem(m, n0 + c + 4 * gg, kv < 4 ? (int)kv : 4, out[gg]);
+            }
           }
           store_unit<Map::GPU>(epi, m, n0 + c, nv < Map::UNIT ? (int)nv : Map::UNIT, out);
         }

@@ -116,8 +116,11 @@ namespace {
 // are taken 8 consecutive tokens of one (kind, head) per wave, chunk by
 // chunk of 8 tokens, so the 2H waves of a chunk read its freqs rows from
 // the cache. A row is read whole before any lane writes it.
+// `kinds` = 2: Q and K (K at epi.koff, normalized with the K weight);
+// 1: one tensor at epi.d with the weight at epi.qw.
 template <bool UNITS>
-__global__ void __launch_bounds__(256) head_norm_rope_kernel(EpiQKVNormRope epi, int64_t H) {
+__global__ void __launch_bounds__(256) head_norm_rope_kernel(EpiQKVNormRope epi, int64_t H,
+                                                             int kinds) {
   using St = Strip<128>;
   using Map = StoreMap<128, uint16_t>;
   __shared__ __attribute__((aligned(16))) float rows[4][St::kBytes / 4];
@@ -126,7 +129,7 @@ __global__ void __launch_bounds__(256) head_norm_rope_kernel(EpiQKVNormRope epi,
   // c of 8 tokens, then (kind, head) t -- a wave reads 2 KB contiguous, and
   // the 2H waves of a chunk share its 8 freqs rows through the cache
   const uint32_t wv = blockIdx.x * 4u + (uint32_t)wave;   // < 2^31 (checked by the host)
-  const uint32_t h2 = (uint32_t)(2 * H);
+  const uint32_t h2 = (uint32_t)(kinds * H);
   const uint32_t c8 = wv / h2, t = wv - c8 * h2;
   const int64_t m = (int64_t)c8 * 8 + prow;
   const bool live = m < epi.rows;
@@ -290,9 +293,64 @@ extern "C" int c4q_i8_gemm_nt_fused_cs_qkv_rms_rope(
   const int64_t blocks = cdiv(cdiv(M, 8) * 2 * H, 4);     // one wave per 8 tokens x (kind, head)
   C4Q_REQUIRE(blocks < (1ll << 29), C4Q_ERR_SHAPE, "%s: problem too large", what);
   if (R % 8 == 0)
-    hipLaunchKernelGGL(head_norm_rope_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, s, epi, H);
+    hipLaunchKernelGGL(head_norm_rope_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, s, epi, H, 2);
   else
-    hipLaunchKernelGGL(head_norm_rope_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, s, epi, H);
+    hipLaunchKernelGGL(head_norm_rope_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, s, epi, H, 2);
+  return check_launch(what);
+}
+
+extern "C" int c4q_i8_gemm_nt_fused_cs_qkv_lora_part(
+    const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb, uint16_t* out,
+    const float* row_scale, const float* col_scale, const uint16_t* bias, const uint16_t* delta,
+    const uint16_t* freqs, const float* norm_weight, int64_t M, int64_t K, int64_t H, int64_t R,
+    int kind, float delta_scale, float eps, void* stream) {
+  const char* what = "c4q_i8_gemm_nt_fused_cs_qkv_lora_part";
+  constexpr int64_t D = 128;
+  C4Q_REQUIRE(kind >= 0 && kind <= 2, C4Q_ERR_ARG, "%s: kind must be Q=0, K=1 or V=2 (got %d)",
+              what, kind);
+  C4Q_REQUIRE(H > 0, C4Q_ERR_SHAPE, "%s: need H > 0 (H=%lld)", what, (long long)H);
+  C4Q_REQUIRE(kind == 2 || (R >= 0 && 2 * R <= D), C4Q_ERR_SHAPE,
+              "%s: need 0 <= 2R <= 128 (R=%lld)", what, (long long)R);
+  const int64_t N = H * D;
+  C4Q_REQUIRE(N < (1ll << 31) && M < (1ll << 31), C4Q_ERR_SHAPE, "%s: problem too large", what);
+  int st = check_i8_args(a, lda, b, ldb, out, N, M, N, K, what);
+  if (st) return st;
+  if (M == 0) return C4Q_OK;
+  C4Q_REQUIRE(aligned16(out), C4Q_ERR_ARG, "%s: out must be 16-byte aligned", what);
+  C4Q_REQUIRE(row_scale != nullptr && col_scale != nullptr, C4Q_ERR_ARG,
+              "%s: null row_scale/col_scale", what);
+  C4Q_REQUIRE(delta != nullptr && (reinterpret_cast<uintptr_t>(delta) & 7u) == 0, C4Q_ERR_ARG,
+              "%s: delta must be non-null and 8-byte aligned", what);
+  if (kind != 2) {
+    C4Q_REQUIRE(norm_weight != nullptr && aligned16(norm_weight), C4Q_ERR_ARG,
+                "%s: norm_weight must be non-null and 16-byte aligned", what);
+    C4Q_REQUIRE(R == 0 || (freqs != nullptr && (reinterpret_cast<uintptr_t>(freqs) & 3u) == 0),
+                C4Q_ERR_ARG, "%s: freqs must be non-null and 4-byte aligned", what);
+  }
+  // the partition's scatter with the delta term, then (Q, K) the in-place
+  // norm/RoPE pass of the two-pass QKV route over the one tensor
+  const float ls = bf16_f32(bf16_rte(delta_scale));
+  EpiQKVLora epi{{{{out, N, 1}, row_scale, col_scale, bias}, 0, 0, M, (uint32_t)N, (uint32_t)D},
+                 delta, ls};
+  hipStream_t s = as_stream(stream);
+  const uint8_t* a8 = reinterpret_cast<const uint8_t*>(a);
+  const uint8_t* b8 = reinterpret_cast<const uint8_t*>(b);
+  const bool tiled = K > 0 && K % 16 == 0 && aligned16(a) && aligned16(b) && lda % 16 == 0 &&
+                     ldb % 16 == 0 && tile_offsets_fit(lda, ldb);
+  const Src2 sa{a8, a8, lda, M}, sb{b8, b8, ldb, N};
+  auto op_for = [](auto t) { return OpI8T<decltype(t)::KS8>{}; };
+  st = tiled ? run_tiles<false>(M, N, N, K, sa, sb, nullptr, epi, s, what, op_for)
+             : launch_generic(M, N, K, GenI8::make(a8, lda, b8, ldb), epi, s, what);
+  if (st || kind == 2) return st;
+  EpiQKVNormRope norm{{{{out, N, 1}, row_scale, col_scale, bias}, 0, 0, M, (uint32_t)N,
+                       (uint32_t)D},
+                      reinterpret_cast<const uint32_t*>(freqs), norm_weight, 0, (int32_t)R, eps};
+  const int64_t blocks = cdiv(cdiv(M, 8) * H, 4);     // one wave per 8 tokens x head
+  C4Q_REQUIRE(blocks < (1ll << 29), C4Q_ERR_SHAPE, "%s: problem too large", what);
+  if (R % 8 == 0)
+    hipLaunchKernelGGL(head_norm_rope_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, s, norm, H, 1);
+  else
+    hipLaunchKernelGGL(head_norm_rope_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, s, norm, H, 1);
   return check_launch(what);
 }
 

@@ -258,6 +258,59 @@ def i8_matmul2d_nt_fused_cs_qkv_rms_rope(a_i8, b_i8, row_scale, col_scale, bias,
     return outs
 
 
+def i8_matmul2d_nt_fused_cs_qkv_lora_part(a_i8, b_i8, row_scale, col_scale, bias, delta, fr,
+                                          norm_weight, heads, head_dim, kind, delta_scale, eps,
+                                          long_schedule=True):
+    """One partition of the H3 QKV projection with a runtime-LoRA delta:
+    b_i8 holds the partition's H*128 weight rows (kind 0 = Q, 1 = K, 2 = V),
+    delta the bf16 low-rank output [M, H*128] for it, added after the bias as
+    ``bf16(value + bf16(delta * bf16(delta_scale)))``; Q and K then get the
+    RMSNorm (fp32 norm_weight) + partial split-half RoPE (fr bf16 [..., M,
+    R, 2, 2]) of the fused QKV route. Returns [1, H, M, 128] bf16
+    (_patches/int8_ext/int8_gemm.mm:2211-2330, kernels :915-1085).
+    long_schedule selects a reference tile order that changes no output
+    byte."""
+    del long_schedule
+    dev, lda, ldb = _i8_operands(a_i8, b_i8)
+    _req(a_i8.is_contiguous() and b_i8.is_contiguous(), "a/b must be contiguous 2D tensors")
+    M, K = a_i8.shape
+    N = b_i8.size(0)
+    _req(M > 64, "H3 QKV specialization requires M > 64")
+    H, D = int(heads), int(head_dim)
+    _req(H > 0 and D == 128 and N == H * D,
+         "LoRA QKV partition requires D=128 and width=H*D")
+    kind = int(kind)
+    _req(0 <= kind <= 2, "kind must be Q=0, K=1 or V=2")
+    _dev(row_scale, col_scale, bias, delta, fr, norm_weight)
+    _vec(row_scale, M, torch.float32, "row_scale")
+    _vec(col_scale, N, torch.float32, "col_scale")
+    _req(delta.dtype == torch.bfloat16 and delta.is_contiguous() and delta.dim() == 2,
+         "LoRA delta must be contiguous bf16 [M,H*D]")
+    _req(tuple(delta.shape) == (M, N), "LoRA delta shape mismatch")
+    _req(fr.dtype == torch.bfloat16 and fr.is_contiguous() and fr.dim() >= 3,
+         "freqs must be contiguous bf16")
+    R = int(fr.size(-3))
+    _req(R > 0 and 2 * R <= D and fr.numel() == M * R * 4, "freqs shape mismatch")
+    _req(norm_weight.dtype == torch.float32 and norm_weight.is_contiguous()
+         and norm_weight.numel() == D, "norm weight must contain D elements")
+    # the kernels read delta 8 bytes, the norm weight 16 and the freqs 4 at a time
+    if delta.data_ptr() % 8:
+        delta = delta.clone()
+    if norm_weight.data_ptr() % 16:
+        norm_weight = norm_weight.clone()
+    if fr.data_ptr() % 4:
+        fr = fr.clone()
+    bias = _bias_bf16(bias, N)
+    out = torch.empty((1, H, M, D), dtype=torch.bfloat16, device=dev)
+    with _on(dev):
+        _lib.call("c4q_i8_gemm_nt_fused_cs_qkv_lora_part", a_i8.data_ptr(), lda, b_i8.data_ptr(),
+                  ldb, out.data_ptr(), row_scale.data_ptr(), col_scale.data_ptr(),
+                  bias.data_ptr() if bias is not None else None, delta.data_ptr(), fr.data_ptr(),
+                  norm_weight.data_ptr(), M, K, H, R, kind, float(delta_scale), float(eps),
+                  _stream(dev))
+    return out
+
+
 # Chunk of FC1 rows of the MLP bridge when the caller asks for "auto": all
 # of them. Measured on MI355X at H3's FC1 (K 5376, W 28672), whole-M FC1
 # GEMMs win over chunks whose bf16 output would stay in the Infinity Cache:

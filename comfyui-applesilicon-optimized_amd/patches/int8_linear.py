@@ -218,21 +218,39 @@ def _plain_int8_layer(layer):
     return w
 
 
+def _runtime_lora(layer, *methods):
+    """The layer's runtime LoRA adapter (the attribute the reference's H3
+    Turbo loader sets): (adapter, ok). ok is False when one is attached but
+    is not a "fast" adapter with every named method -- the routes then
+    decline the layer so the adapter's own forward hook keeps it."""
+    adapter = getattr(layer, _RUNTIME_LORA_ATTR, None)
+    if adapter is None:
+        return None, True
+    ok = bool(getattr(adapter, "fast", False)) and all(hasattr(adapter, m) for m in methods)
+    return adapter, ok
+
+
 def _int8_qkv_prequant(layer, x, heads, head_dim, norm_rope):
     """The H3 QKV projection straight into the attention layout (reference
     ``_int8_qkv_prequant``, ``:266-412``): [Q, K, V], each [1, H, S, D]
     bf16, or None when a check fails (the caller then runs the layer and
     splits heads itself). ``norm_rope`` is None (layout only) or
     (freqs, q_weight, k_weight, eps) for the D = 128 RMSNorm + partial RoPE
-    epilogue. Runtime LoRA adapters and ConvRot weights are not served
-    (None). Switches: ``C4Q_INT8_QKV_SCATTER=0`` / ``C4Q_INT8_QKV_NORM_ROPE=0``
-    (or the reference's ``ASFP8_`` names)."""
+    epilogue. ConvRot weights quantize x through the rotate + quant pass.
+    A fast runtime LoRA adapter is served: with norm/RoPE, one partition
+    kernel per Q, K, V adds its bf16 delta before the norm (the adapter's
+    ``linear_parts``); without, its ``add_qkv_to`` updates the scattered
+    Q, K, V. Switches: ``C4Q_INT8_QKV_SCATTER=0`` /
+    ``C4Q_INT8_QKV_NORM_ROPE=0`` (or the reference's ``ASFP8_`` names)."""
     def _on(name):
         return os.environ.get("C4Q_" + name, os.environ.get("ASFP8_" + name, "1")) == "1"
 
-    if not _on("INT8_QKV_SCATTER") or (norm_rope is not None and not _on("INT8_QKV_NORM_ROPE")):
+    fused_norm_rope = norm_rope is not None
+    if not _on("INT8_QKV_SCATTER") or (fused_norm_rope and not _on("INT8_QKV_NORM_ROPE")):
         return None
-    if getattr(layer, _RUNTIME_LORA_ATTR, None) is not None:
+    runtime_lora, ok = _runtime_lora(layer, "add_qkv_to")
+    lora_norm_rope = fused_norm_rope and runtime_lora is not None
+    if not ok or (lora_norm_rope and not hasattr(runtime_lora, "linear_parts")):
         return None
     if (not isinstance(x, torch.Tensor) or x.dim() != 2 or not _common.on_device(x)
             or x.dtype != torch.bfloat16 or not x.is_contiguous()):
@@ -241,30 +259,56 @@ def _int8_qkv_prequant(layer, x, heads, head_dim, norm_rope):
     if w is None:
         return None
     params = w._params
-    if getattr(params, "convrot", False):
-        return None
     qdata = w._qdata
     if tuple(qdata.shape) != (3 * heads * head_dim, x.shape[1]):
         return None
     weight_scale = params.scale.reshape(-1)
     if weight_scale.numel() != qdata.shape[0]:
         return None
+    convrot = bool(getattr(params, "convrot", False))
+    groupsize = getattr(params, "convrot_groupsize", 256)
+    if convrot and not _convrot_ok(x, groupsize):
+        return None
     try:
-        x_8, x_scale = _quant_cached(x)
+        x_8, x_scale = _quant_cached(x, convrot, groupsize)
         bias = layer.bias
         bias_arg = bias.to(torch.bfloat16) if bias is not None else None
-        common = (x_8, qdata.contiguous(), x_scale.reshape(-1).float().contiguous(),
-                  weight_scale.float().contiguous(), bias_arg)
-        if norm_rope is None:
-            return ops.i8_matmul2d_nt_fused_cs_qkv(*common, heads, head_dim)
+        rs = x_scale.reshape(-1).float().contiguous()
+        cs = weight_scale.float().contiguous()
+        if not fused_norm_rope:
+            qkv = ops.i8_matmul2d_nt_fused_cs_qkv(x_8, qdata.contiguous(), rs, cs, bias_arg,
+                                                  heads, head_dim)
+            if runtime_lora is not None:
+                qkv = list(runtime_lora.add_qkv_to(*qkv, x, heads, head_dim))
+            return qkv
         freqs, q_weight, k_weight, eps = norm_rope
         if (not isinstance(freqs, torch.Tensor) or not isinstance(q_weight, torch.Tensor)
                 or not isinstance(k_weight, torch.Tensor)):
             return None
-        return ops.i8_matmul2d_nt_fused_cs_qkv_rms_rope(*common, freqs, q_weight, k_weight,
-                                                        heads, head_dim, float(eps))
+        if runtime_lora is None:
+            return ops.i8_matmul2d_nt_fused_cs_qkv_rms_rope(
+                x_8, qdata.contiguous(), rs, cs, bias_arg, freqs, q_weight, k_weight, heads,
+                head_dim, float(eps))
+        # reference :351-379: the low-rank product once, then per partition
+        # its delta [M, H D] and the partition kernel
+        up, down, lora_scale = runtime_lora.linear_parts(x)
+        width = heads * head_dim
+        if up.shape[0] != 3 * width or up.shape[1] != down.shape[0] or down.shape[1] != x.shape[1]:
+            return None
+        low_rank = torch.nn.functional.linear(x, down)
+        outputs = []
+        for kind in range(3):
+            lo, hi = kind * width, (kind + 1) * width
+            delta = torch.nn.functional.linear(low_rank, up[lo:hi]).contiguous()
+            part_bias = bias_arg[lo:hi].contiguous() if bias_arg is not None else None
+            outputs.append(ops.i8_matmul2d_nt_fused_cs_qkv_lora_part(
+                x_8, qdata[lo:hi].contiguous(), rs, cs[lo:hi].contiguous(), part_bias, delta,
+                freqs, k_weight if kind == 1 else q_weight, heads, head_dim, kind,
+                float(lora_scale), float(eps)))
+            del delta
+        return outputs
     except C4QError as e:
-        route = "qkv norm/RoPE epilogue" if norm_rope is not None else "qkv scatter"
+        route = "qkv norm/RoPE epilogue" if fused_norm_rope else "qkv scatter"
         print(f"{TAG} {route} fell back ({e})")
         return None
 
@@ -288,8 +332,13 @@ def int8_o_proj_prequant(layer, out_bhsd):
     always the fused butterfly pass -- the reference's mode "2"; its mode "1"
     for D = 256 rotates with comfy_kitchen's eager Hadamard matmul, which this
     build does not have (same rounding class, different fp32 sum order).
+    A fast runtime LoRA adapter's ``add_bhsd_to`` adds its delta to the
+    result; a slow one makes the route decline.
     ``C4Q_INT8_OPROJ_FUSE=0`` (or the reference's ``ASFP8_INT8_OPROJ_FUSE=0``)
     turns it off."""
+    runtime_lora, ok = _runtime_lora(layer)
+    if not ok:
+        return None
     mode = os.environ.get("C4Q_INT8_OPROJ_FUSE", os.environ.get("ASFP8_INT8_OPROJ_FUSE", "1"))
     if mode == "0":
         return None
@@ -307,24 +356,35 @@ def int8_o_proj_prequant(layer, out_bhsd):
     if D <= 0 or D > 256 or (H * D) % 256 or H * D * 2 > 30 * 1024 or H * D != qdata.shape[1]:
         return None
     x_8, x_scale = ops.i8_merge_rot_quant(out_bhsd.contiguous())
-    return _int8_linear_prequant(x_8, x_scale, qdata.contiguous(), params.scale, layer.bias,
-                                 torch.bfloat16, (B, S, H * D))
+    r = _int8_linear_prequant(x_8, x_scale, qdata.contiguous(), params.scale, layer.bias,
+                              torch.bfloat16, (B, S, H * D))
+    if runtime_lora is not None:
+        # this route bypasses Linear.forward, so the adapter's delta is added
+        # here (reference :527-531)
+        r = runtime_lora.add_bhsd_to(r, out_bhsd)
+    return r
 
 
 def int8_mlp_bridge(fc1, fc2, x):
     """H3 INT8 FC1 -> SwiGLU -> ConvRot -> FC2 without storing FC1's [M, 2F]
     output whole (reference ``:538-673``): x [M, K] bf16 -> [M, N2] bf16, or
-    None when a check fails. FC1 runs chunk by chunk through the bridge
+    None when a check fails. FC1 runs through the bridge
     (``ops.i8_mlp_bridge_prequant``), FC2 on its quantized activation.
     Requires per-channel scales on both layers and a ConvRot FC2 (group
-    256); runtime LoRA adapters are not served. Switches:
-    ``C4Q_INT8_MLP_BRIDGE=0`` (or ``ASFP8_INT8_MLP_BRIDGE``,
-    ``ASFP8_INT8_SWIGLU``, ``ASFP8_INT8_SWIGLU_ROT`` = 0)."""
+    256). With fast runtime LoRA adapters on FC1 and/or FC2 the rows go in
+    tiles (``ASFP8_INT8_MLP_LORA_TILE_ROWS``, default 2048): FC1's fused_cs
+    output plus its scaled delta, the bf16 SwiGLU, FC2's low-rank input
+    from that activation, its rotation + quant; FC2's delta is added to the
+    result (reference ``:604-658``). Switches: ``C4Q_INT8_MLP_BRIDGE=0`` (or
+    ``ASFP8_INT8_MLP_BRIDGE``, ``ASFP8_INT8_SWIGLU``,
+    ``ASFP8_INT8_SWIGLU_ROT`` = 0)."""
     if (os.environ.get("C4Q_INT8_MLP_BRIDGE", os.environ.get("ASFP8_INT8_MLP_BRIDGE", "1")) != "1"
             or os.environ.get("ASFP8_INT8_SWIGLU", "1") != "1"
             or os.environ.get("ASFP8_INT8_SWIGLU_ROT", "1") != "1"):
         return None
-    if any(getattr(layer, _RUNTIME_LORA_ATTR, None) is not None for layer in (fc1, fc2)):
+    lora1, ok1 = _runtime_lora(fc1, "linear_parts")
+    lora2, ok2 = _runtime_lora(fc2, "linear_parts")
+    if not (ok1 and ok2):
         return None
     if (not isinstance(x, torch.Tensor) or x.dim() != 2 or not _common.on_device(x)
             or x.dtype != torch.bfloat16 or not x.is_contiguous()):
@@ -349,11 +409,52 @@ def int8_mlp_bridge(fc1, fc2, x):
     try:
         x_8, x_scale = _quant_cached(x, convrot1, gs1)
         bias1 = fc1.bias.to(torch.bfloat16) if fc1.bias is not None else None
-        fc2_8, fc2_scale = ops.i8_mlp_bridge_prequant(
-            x_8.contiguous(), q1.contiguous(), x_scale.reshape(-1).float().contiguous(),
-            s1.float().contiguous(), bias1)
-        return _int8_linear_prequant(fc2_8, fc2_scale, q2, s2, fc2.bias, x.dtype, x.shape,
-                                     split_tail=True)
+        if lora1 is None and lora2 is None:
+            fc2_8, fc2_scale = ops.i8_mlp_bridge_prequant(
+                x_8.contiguous(), q1.contiguous(), x_scale.reshape(-1).float().contiguous(),
+                s1.float().contiguous(), bias1)
+            return _int8_linear_prequant(fc2_8, fc2_scale, q2, s2, fc2.bias, x.dtype, x.shape,
+                                         split_tail=True)
+        linear = torch.nn.functional.linear
+        rows, ffn = x.shape[0], q2.shape[1]
+        parts1 = lora1.linear_parts(x) if lora1 is not None else None
+        parts2 = lora2.linear_parts(x) if lora2 is not None else None
+        if parts1 is not None:
+            up1, down1, scale1 = parts1
+            if tuple(up1.shape) != (2 * ffn, down1.shape[0]) or down1.shape[1] != x.shape[1]:
+                return None
+            low1 = linear(x, down1)
+        if parts2 is not None:
+            up2, down2, scale2 = parts2
+            if tuple(up2.shape) != (q2.shape[0], down2.shape[0]) or down2.shape[1] != ffn:
+                return None
+            low2 = torch.empty((rows, down2.shape[0]), device=x.device, dtype=x.dtype)
+        fc2_8 = torch.empty((rows, ffn), device=x.device, dtype=torch.int8)
+        fc2_scale = torch.empty((rows, 1), device=x.device, dtype=torch.float32)
+        tile_rows = max(128, int(os.environ.get("ASFP8_INT8_MLP_LORA_TILE_ROWS", "2048")))
+        tile_rows = tile_rows // 128 * 128
+        row_scales = x_scale.reshape(-1).float().contiguous()
+        col_scales = s1.float().contiguous()
+        q1c = q1.contiguous()
+        for lo in range(0, rows, tile_rows):
+            hi = min(lo + tile_rows, rows)
+            wide = ops.i8_matmul2d_nt_fused_cs(x_8[lo:hi].contiguous(), q1c,
+                                               row_scales[lo:hi].contiguous(), col_scales, bias1)
+            if parts1 is not None:
+                wide.add_(linear(low1[lo:hi], up1), alpha=scale1)
+            act = _swiglu_activation(wide)
+            del wide
+            if parts2 is not None:
+                low2[lo:hi].copy_(linear(act, down2))
+            act_8, act_scale = _quant_cached(act, True, 256)
+            fc2_8[lo:hi].copy_(act_8)
+            fc2_scale[lo:hi].copy_(act_scale.reshape(-1, 1))
+            del act, act_8, act_scale
+        result = _int8_linear_prequant(fc2_8, fc2_scale, q2, s2, fc2.bias, x.dtype, x.shape,
+                                       split_tail=True)
+        if parts2 is not None:
+            result.add_(linear(low2, up2), alpha=scale2)
+        return result
     except C4QError as e:
         print(f"{TAG} MLP bridge fell back ({e})")
         return None
@@ -364,12 +465,15 @@ def _try_int8_swiglu_forward(linear, x):
     With a ConvRot weight (group size 256) and a contiguous bf16 input: the
     fused SwiGLU + rotation pass, rowwise quant, the INT8 GEMM; without
     ConvRot: the bf16 SwiGLU (torch ops) and the ordinary kernel path.
-    Layers with a runtime LoRA adapter are not served (the caller's
-    ``linear(swiglu(x))`` keeps the adapter); a call the kernels reject
+    With a fast runtime LoRA adapter the bf16 SwiGLU activation is formed
+    once, the INT8 path projects it and the adapter's ``add_to`` adds its
+    delta from that activation (a slow adapter makes the route decline, so
+    the caller's ``linear(swiglu(x))`` keeps it); a call the kernels reject
     falls back too."""
     if not _common.on_device(x) or _common.is_quantized_int8(x):
         return None
-    if getattr(linear, _RUNTIME_LORA_ATTR, None) is not None:
+    runtime_lora, ok = _runtime_lora(linear)
+    if not ok:
         return None
     w = _plain_int8_layer(linear)
     if w is None:
@@ -380,6 +484,12 @@ def _try_int8_swiglu_forward(linear, x):
     half = wide // 2
     params = w._params
     try:
+        if runtime_lora is not None:
+            act = _swiglu_activation(x)
+            base = _int8_linear_kernel(act, w._qdata, params.scale, linear.bias, x.dtype,
+                                       bool(getattr(params, "convrot", False)),
+                                       getattr(params, "convrot_groupsize", 256))
+            return runtime_lora.add_to(base, act)
         if getattr(params, "convrot", False):
             x2 = x.reshape(-1, wide)
             if (getattr(params, "convrot_groupsize", 256) != 256 or x.dtype != torch.bfloat16

@@ -116,6 +116,25 @@ int c4q_i8_gemm_nt_fused_cs_qkv_rms_rope(const int8_t* a, int64_t lda, const int
                                          int64_t M, int64_t K, int64_t H, int64_t R, float eps,
                                          void* stream);
 
+/* H3 runtime-LoRA partition, D = 128: one of Q (kind 0), K (1) or V (2),
+ * i.e. the partition's H*128 weight rows b, projected and stored as
+ * out[1, H, M, 128] like the QKV scatter, with a bf16 low-rank delta
+ * [M, H*128] (rows contiguous, 8-byte aligned) added after the bias:
+ *   sd = bf16(f32(delta[m,n]) * f32(bf16(delta_scale))), value = bf16(value + sd)
+ * then, for Q and K, the RMSNorm + partial RoPE of the variant above with
+ * norm_weight f32[128] (16-byte aligned) and freqs bf16 [M, R, 2, 2].
+ * out 16-byte aligned. Replaces i8_matmul2d_nt_fused_cs_qkv_lora_part
+ * (_patches/int8_ext/int8_gemm.mm:2211-2330, kernels :915-1085) behind
+ * _int8_qkv_prequant's runtime-LoRA route
+ * (_patches/int8_linear_kernel_mps.py:351-379). */
+int c4q_i8_gemm_nt_fused_cs_qkv_lora_part(const int8_t* a, int64_t lda, const int8_t* b,
+                                          int64_t ldb, uint16_t* out, const float* row_scale,
+                                          const float* col_scale, const uint16_t* bias,
+                                          const uint16_t* delta, const uint16_t* freqs,
+                                          const float* norm_weight, int64_t M, int64_t K,
+                                          int64_t H, int64_t R, int kind, float delta_scale,
+                                          float eps, void* stream);
+
 /* Rowwise int8 activation quant of x[M,K] (bf16 or f16):
  * q[M,K] int8 and scales[M] fp32, bit-exact with comfy_kitchen
  * quantize_int8_rowwise. Replaces i8_quant_rowwise

@@ -84,6 +84,26 @@ def scatter_qkv(d_bits, heads, head_dim):
     return [np.ascontiguousarray(x[k][None]) for k in range(3)]
 
 
+def lora_delta_add(d_bits, delta_bits, delta_scale):
+    """Runtime-LoRA delta term of the H3 partition epilogue, added to the
+    bf16 projection value d (after its bias): ls = bf16(delta_scale),
+    sd = bf16(f32(delta) * f32(ls)), out = bf16(f32(d) + f32(sd)).
+    Reference ``_patches/int8_ext/int8_gemm.mm:947,966-968`` (Q/K) and
+    ``:1048,1062-1064`` (V); delta_scale arrives as a float32
+    (``float ds = (float)delta_scale``, ``:2297``)."""
+    ls = bf16_bits_to_f32(f32_to_bf16_bits(np.asarray([delta_scale], dtype=F32)))[0]
+    sd = f32_to_bf16_bits(bf16_bits_to_f32(delta_bits) * ls)
+    return f32_to_bf16_bits(bf16_bits_to_f32(d_bits) + bf16_bits_to_f32(sd))
+
+
+def scatter_part(d_bits, heads, head_dim):
+    """One partition [M, H D] -> [1, H, M, D]: column h*D + d to
+    out[0, h, m, d] (reference ``int8_gemm.mm:1065-1068``)."""
+    d = np.asarray(d_bits)
+    m = d.shape[0]
+    return np.ascontiguousarray(d.reshape(m, heads, head_dim).transpose(1, 0, 2)[None])
+
+
 BF16_TINY = F32(2.0 ** -126)   # torch.finfo(torch.bfloat16).tiny
 F16_TINY = F32(2.0 ** -14)     # torch.finfo(torch.float16).tiny
 

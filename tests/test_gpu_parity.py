@@ -176,8 +176,8 @@ def test_f16_outputs_round_f32_results_once(dev):
 # ConvRot: fused head merge + 256-wide rotation + rowwise quant
 MRQ_CASES = [(1, 24, 300, 128), (1, 12, 257, 256), (2, 3, 50, 256), (1, 8, 33, 96),
              (1, 1, 5, 256), (1, 120, 3, 128), (1, 64, 9, 100),   # D=100: 2-byte gathers
-             # more rows than the persistent grid holds: each workgroup loops over
-             # rows with the next row's gather in flight
+             # one workgroup per row: far more workgroups than the device holds at
+             # once, so they run in several waves of residency
              (1, 2, 6000, 128), (2, 12, 1100, 256)]
 
 
@@ -382,6 +382,75 @@ def test_i8_fused_cs_qkv_rms_rope_generic_path(dev, M, K, H, R):
         ref = oqk.qkv_rms_rope(*pre, bits16(ins[5]), ins[6].numpy(), ins[7].numpy(), 1e-6)
     for name, o, r in zip("qkv", outs, ref):
         assert_bits_equal(bits16(o), r, f"qkv-rms-rope generic {name} {M}x{K} H{H} R{R}")
+
+
+@pytest.mark.parametrize("tile", [None, "5", "7"])
+@pytest.mark.parametrize("kind", [0, 1, 2])
+@pytest.mark.parametrize("M,K,H,R,bias,scale", [(300, 1024, 4, 48, True, 0.3),
+                                                (777, 512, 3, 20, False, 1.0),
+                                                (130, 200, 2, 48, True, 0.0123),  # generic path
+                                                (2100, 640, 7, 64, True, 2.5)])
+def test_i8_qkv_lora_part_exact(dev, monkeypatch, tile, kind, M, K, H, R, bias, scale):
+    """H3 runtime-LoRA partition: the partition's fused_cs bytes plus the
+    rounded delta term, scattered to [1, H, M, 128]; Q and K then through
+    the RMSNorm + partial RoPE -- bit-exact to the oracle chain, on the
+    default tile plan and with the 64x128 and split-K tiles forced."""
+    if tile is not None:
+        monkeypatch.setenv("C4Q_TILE", tile)
+    g = gen(17 + M + H + R + kind)
+    N = H * 128
+    a, b = _randint8((M, K), g), _randint8((N, K), g)
+    rs = torch.rand(M, generator=g) * 0.01
+    cs = torch.rand(N, generator=g) * 0.02
+    bb = torch.randn(N, generator=g).to(torch.bfloat16) if bias else None
+    delta = (torch.randn(M, N, generator=g) * 0.5).to(torch.bfloat16)
+    freqs = torch.randn(1, M, 1, R, 2, 2, generator=g).to(torch.bfloat16)
+    nw = (1 + torch.randn(128, generator=g) * 0.1).float()
+    base = oi.epilogue_rowcolscale(oi.i8_matmul2d_nt(a.numpy(), b.numpy()), rs.numpy(),
+                                   cs.numpy(), bits16(bb) if bias else None)
+    ref = oi.scatter_part(oi.lora_delta_add(base, bits16(delta), scale), H, 128)
+    if kind != 2:
+        ref = oqk.qk_rms_rope(ref, bits16(freqs), nw.numpy(), 1e-6)
+    out = ops.i8_matmul2d_nt_fused_cs_qkv_lora_part(
+        a.to(dev), b.to(dev), rs.to(dev), cs.to(dev), bb.to(dev) if bias else None,
+        delta.to(dev), freqs.to(dev), nw.to(dev), H, 128, kind, scale, 1e-6)
+    assert out.shape == (1, H, M, 128)
+    assert_bits_equal(bits16(out), ref, f"qkv lora part kind {kind} {M}x{K} H{H} R{R} tile {tile}")
+
+
+def test_i8_qkv_lora_part_zero_delta_is_the_scatter_route(dev):
+    """With a zero delta the partitions equal the QKV + norm/RoPE route's
+    Q, K and V (the delta term then adds +0 and rounds nothing)."""
+    M, K, H, R = 512, 1024, 6, 48
+    ins, _ = _qkv_rope_case(M, K, H, R, 23)
+    a, b, rs, cs, bb, freqs, qw, kw = (t.to(dev) for t in ins)
+    full = ops.i8_matmul2d_nt_fused_cs_qkv_rms_rope(a, b, rs, cs, bb, freqs, qw, kw, H, 128, 1e-6)
+    zero = torch.zeros(M, H * 128, dtype=torch.bfloat16, device=dev)
+    w = H * 128
+    for kind in range(3):
+        part = ops.i8_matmul2d_nt_fused_cs_qkv_lora_part(
+            a, b[kind * w:(kind + 1) * w].contiguous(), rs, cs[kind * w:(kind + 1) * w].contiguous(),
+            bb[kind * w:(kind + 1) * w].contiguous(), zero, freqs, kw if kind == 1 else qw,
+            H, 128, kind, 0.7, 1e-6)
+        assert torch.equal(part, full[kind]), f"kind {kind}"
+
+
+def test_i8_qkv_lora_part_rejects_bad_arguments(dev):
+    g = gen(3)
+    M, K, H = 100, 256, 2
+    a, b = _randint8((M, K), g).to(dev), _randint8((H * 128, K), g).to(dev)
+    rs, cs = torch.ones(M, device=dev), torch.ones(H * 128, device=dev)
+    delta = torch.zeros(M, H * 128, dtype=torch.bfloat16, device=dev)
+    fr = torch.zeros(M, 8, 2, 2, dtype=torch.bfloat16, device=dev)
+    nw = torch.ones(128, device=dev)
+    call = ops.i8_matmul2d_nt_fused_cs_qkv_lora_part
+    with pytest.raises(C4QError, match="kind"):
+        call(a, b, rs, cs, None, delta, fr, nw, H, 128, 3, 1.0, 1e-6)
+    with pytest.raises(C4QError, match="delta shape"):
+        call(a, b, rs, cs, None, delta[:, :128].contiguous(), fr, nw, H, 128, 0, 1.0, 1e-6)
+    with pytest.raises(C4QError, match="M > 64"):
+        call(a[:64].contiguous(), b, rs[:64].contiguous(), cs, None, delta[:64].contiguous(),
+             fr[:64].contiguous(), nw, H, 128, 0, 1.0, 1e-6)
 
 
 def test_i8_fused_cs_qkv_rms_rope_matches_scatter_then_norm(dev):

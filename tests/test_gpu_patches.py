@@ -282,6 +282,92 @@ def test_qkv_prequant_routes_exact(dev):
         assert_bits_equal(bits16(o), r, f"qkv rms-rope patch {name}")
 
 
+def test_qkv_runtime_lora_route_exact(dev):
+    """The H3 QKV + norm/RoPE route with a fast runtime LoRA adapter on the
+    device: the low-rank deltas come from torch on the GPU (the route's own
+    calls), the rest is the oracle chain -- per partition the fused_cs value,
+    the rounded delta term, the scatter, Q/K norm + RoPE -- bit-exact."""
+    import torch.nn.functional as F
+    from oracle import qknorm as oqk
+
+    class QT:
+        _layout_cls = "TensorWiseINT8Layout"
+
+        def __init__(self, q, scale):
+            self._qdata = q
+            self._params = types.SimpleNamespace(scale=scale, convrot=False, transposed=False)
+
+    class Adapter:
+        fast = True
+
+        def __init__(self, up, down, scale):
+            self.up, self.down, self.scale = up, down, scale
+
+        def linear_parts(self, x):
+            return self.up, self.down, self.scale
+
+        def add_qkv_to(self, q, k, v, x, heads, head_dim):
+            raise AssertionError("the norm/RoPE route uses the partition kernel")
+
+    g = gen(37)
+    S, K, H, D, R, rank = 200, 512, 3, 128, 48, 8
+    x = (torch.randn(S, K, generator=g) * 2).to(torch.bfloat16)
+    w = _i8((3 * H * D, K), g)
+    ws = torch.rand(3 * H * D, generator=g) * 0.002
+    bias = (torch.randn(3 * H * D, generator=g) * 0.1).to(torch.bfloat16)
+    fr = torch.randn(1, S, 1, R, 2, 2, generator=g).to(torch.bfloat16)
+    qw = (1 + torch.randn(D, generator=g) * 0.1).float()
+    kw = (1 + torch.randn(D, generator=g) * 0.1).float()
+    up = (torch.randn(3 * H * D, rank, generator=g) * 0.2).to(torch.bfloat16).to(dev)
+    down = (torch.randn(rank, K, generator=g) * 0.2).to(torch.bfloat16).to(dev)
+    layer = types.SimpleNamespace(weight=QT(w.to(dev), ws.to(dev)), bias=bias.to(dev),
+                                  weight_function=[], bias_function=[],
+                                  _asfp8_runtime_lora=Adapter(up, down, 0.75))
+    xd = x.to(dev)
+    outs = int8_linear.int8_qkv_rms_rope_prequant(layer, xd, fr.to(dev), qw.to(dev), kw.to(dev),
+                                                  H, D, 1e-6)
+    xq, xs = oi.quant_rowwise(bits16(x), "bf16")
+    base = oi.epilogue_rowcolscale(oi.i8_matmul2d_nt(xq, w.numpy()), xs.reshape(-1), ws.numpy(),
+                                   bits16(bias))
+    low = F.linear(xd, down)
+    width = H * D
+    for kind, name in enumerate("qkv"):
+        cols = slice(kind * width, (kind + 1) * width)
+        delta = bits16(F.linear(low, up[cols]).cpu())
+        ref = oi.scatter_part(oi.lora_delta_add(base[:, cols], delta, 0.75), H, D)
+        if kind != 2:
+            ref = oqk.qk_rms_rope(ref, bits16(fr), (kw if kind == 1 else qw).numpy(), 1e-6)
+        assert_bits_equal(bits16(outs[kind]), ref, f"qkv lora patch {name}")
+
+
+def test_qkv_route_convrot_exact(dev):
+    """A ConvRot QKV weight: x rotated + quantized by the fused pass, then
+    the QKV scatter -- bit-exact against the oracle chain."""
+    from oracle import convrot as ocr
+
+    class QT:
+        _layout_cls = "TensorWiseINT8Layout"
+
+        def __init__(self, q, scale):
+            self._qdata = q
+            self._params = types.SimpleNamespace(scale=scale, convrot=True, transposed=False,
+                                                 convrot_groupsize=256)
+
+    g = gen(39)
+    S, K, H, D = 150, 512, 2, 128
+    x = (torch.randn(S, K, generator=g) * 2).to(torch.bfloat16)
+    w = _i8((3 * H * D, K), g)
+    ws = torch.rand(3 * H * D, generator=g) * 0.002
+    layer = types.SimpleNamespace(weight=QT(w.to(dev), ws.to(dev)), bias=None,
+                                  weight_function=[], bias_function=[])
+    outs = int8_linear.int8_qkv_prequant(layer, x.to(dev), H, D)
+    rq, rs = ocr.merge_rot_quant(bits16(x).reshape(S, K // 256, 1, 256))   # the product's view
+    pre = oi.scatter_qkv(oi.epilogue_rowcolscale(oi.i8_matmul2d_nt(rq, w.numpy()), rs.reshape(-1),
+                                                 ws.numpy()), H, D)
+    for name, o, r in zip("qkv", outs, pre):
+        assert_bits_equal(bits16(o), r, f"qkv convrot patch {name}")
+
+
 def test_mlp_bridge_route_exact(dev):
     """int8_mlp_bridge(fc1, fc2, x) on stand-in TensorWiseINT8Layout weights
     (FC2 ConvRot): the FC2 output of the oracle chain, bit-exact."""

@@ -478,6 +478,42 @@ def test_scatter_qkv_is_the_torch_split_and_head_transpose():
         assert np.array_equal(a, tbits(b))
 
 
+@pytest.mark.parametrize("scale", [1.0, 0.3, 0.0123, 5.7])
+def test_lora_delta_add_is_torch_bf16_mul_then_add(scale):
+    """The runtime-LoRA term against torch's CPU bf16 ops, which round each
+    operation: value + delta * bf16(scale)."""
+    g = torch.Generator().manual_seed(46)
+    base = (torch.randn(64, 96, generator=g) * 4).to(torch.bfloat16)
+    delta = (torch.randn(64, 96, generator=g) * 0.05).to(torch.bfloat16)
+    base[0, :4] = torch.tensor([0.0, -0.0, 3.0e38, -1.0e-40]).to(torch.bfloat16)
+    ls = torch.tensor(scale, dtype=torch.float32).to(torch.bfloat16)
+    want = base + delta * ls
+    got = oi.lora_delta_add(tbits(base), tbits(delta), scale)
+    assert np.array_equal(got, tbits(want))
+
+
+def test_lora_delta_add_rounds_the_scaled_delta_and_the_scale():
+    """Dropping either intermediate rounding (the bf16 scale, the bf16
+    scaled delta) changes some outputs, so the pin above sees both."""
+    g = torch.Generator().manual_seed(47)
+    base = (torch.randn(4096, generator=g) * 4).to(torch.bfloat16)
+    delta = (torch.randn(4096, generator=g) * 0.5).to(torch.bfloat16)
+    got = oi.lora_delta_add(tbits(base), tbits(delta), 0.3)
+    fused = (base.float() + delta.float() * torch.tensor(0.3).to(torch.bfloat16).float()).to(
+        torch.bfloat16)
+    raw_scale = (base.float() + (delta.float() * 0.3).to(torch.bfloat16).float()).to(torch.bfloat16)
+    assert not np.array_equal(got, tbits(fused))
+    assert not np.array_equal(got, tbits(raw_scale))
+
+
+def test_scatter_part_is_the_torch_head_transpose():
+    g = torch.Generator().manual_seed(48)
+    m, h, d = 5, 3, 8
+    y = torch.randn(m, h * d, generator=g).to(torch.bfloat16)
+    want = y.reshape(m, h, d).transpose(0, 1).unsqueeze(0).contiguous()
+    assert np.array_equal(oi.scatter_part(tbits(y), h, d), tbits(want))
+
+
 # ------------------------------------------------ Q/K RMSNorm + RoPE (H3) ---
 
 def _qk_inputs(seed, rows=37, heads=2, pairs=48):

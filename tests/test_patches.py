@@ -559,11 +559,12 @@ def test_fp8_ext_functions_route_to_w8a16(monkeypatch):
 
 
 def test_loader_surface_names():
-    """Every function the reference's three native modules export (except
-    the runtime-LoRA QKV part) exists in ops under the same name."""
+    """Every function the reference's three native modules export exists in
+    ops under the same name."""
     names = ["i8_mlp_bridge_prequant", "i8_swiglu_rot", "i8_merge_rot_quant",
              "i8_matmul2d_nt_fused_cs", "i8_matmul2d_nt_fused_cs_half",
              "i8_matmul2d_nt_fused_cs_qkv", "i8_matmul2d_nt_fused_cs_qkv_rms_rope",
+             "i8_matmul2d_nt_fused_cs_qkv_lora_part",
              "i8_quant_rowwise", "i8_matmul2d_nt", "i8_matmul2d_nt_fused", "warmup",
              "fp8_matmul2d", "fp8_matmul2d_nt", "fp8fp8_matmul2d_nt",
              "w8a16_f32", "w8a16_bias_bf16", "num_variants"]
