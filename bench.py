@@ -128,7 +128,8 @@ def bench_c2(torch, ops, dev, steps, warmup):
     return {
         "flops": flops, "wall_s": wall, "tflops": flops / wall / 1e12,
         "kernel": ("W8A16 GEMM fused-QKV 9216x3072 -> 9216: 1280 tiles of 256x256 "
-                   "(ping-pong schedule) + 16 leftover tiles as 256 split-K pieces of 64x64"),
+                   "(one wave per SIMD, 4 waves of 256x64) + 16 leftover tiles as 256 split-K "
+                   "pieces of 64x64"),
         "kernel_s": kern, "kernel_flops": qkv_flops,
         "kernel_tflops": qkv_flops / kern / 1e12 if kern else None,
     }
@@ -509,7 +510,7 @@ def bench_c5(torch, ops, dev, steps, warmup):
 # the default run reports as roofline.traffic.
 COPY_BYTES = 512 * 1024 * 1024
 TRAFFIC_FILE = ROOT / "profiles" / "w8a16_gemm_c2_qkv_traffic.json"
-QKV_KERNEL_KEY = "OpW8A16"
+QKV_KERNEL_KEY = "EpiW8A16"     # in the names of the main (gemm_w4a16_kernel) and tail launches
 PMC_CALLS = 3
 SOURCE_FILES = ("comfyui-applesilicon-optimized_amd/csrc", "include")
 

@@ -541,7 +541,6 @@ struct StoreMap {
 template <int GPU, class Epi, class Packed>
 __device__ __forceinline__ void store_unit(const Epi& epi, int64_t m, int64_t n, int nv,
                                            const Packed* p) {
-  using OutT = typename Epi::OutT;
   if (epi.vec && nv >= 4 * GPU) {
     uint8_t* dst = epi.addr(m, n);
     if constexpr (sizeof(Packed) == 8 && GPU == 2)
@@ -1368,7 +1367,6 @@ gemm_w4_kernel(GemmShape sh, Src2 sa, Src2 sb, const float* b_scale, Epi epi) {
   const Epi ep = epi.prepare();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform
   const int wm = wave / WN, wn = wave % WN;
-  const float ws = Op::prep_scale(b_scale);
 
   LA la;
   LB lb;
