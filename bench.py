@@ -167,11 +167,7 @@ def cpu_baseline_c2(torch, budget_s=12.0):
     times = [t1] + [run(rows) for _ in range(reps - 1)]
     tmed = statistics.median(times)
     flops = sum(2.0 * rows * K * n for n in Ns)
-    try:
-        model = next((l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo")
-                      if l.startswith("model name")), "unknown")
-    except OSError:
-        model = "unknown"
+    model = _cpu_model()
     return {
         "value": flops / tmed / 1e12, "unit": "TFLOP/s", "cores": torch.get_num_threads(),
         "kind": "port",
@@ -179,6 +175,23 @@ def cpu_baseline_c2(torch, budget_s=12.0):
                    f"weights dequantized per call), median of {reps} reps = {tmed:.3f} s; "
                    f"torch CPU, {model}"),
     }
+
+
+def _cpu_model():
+    """The host CPU as /proc/cpuinfo names it, with its CPUID family / model /
+    stepping (a virtual machine may report only the brand name)."""
+    try:
+        info = {}
+        for line in open("/proc/cpuinfo"):
+            if ":" in line:
+                k, v = line.split(":", 1)
+                info.setdefault(k.strip(), v.strip())
+            elif info:
+                break                     # first processor's block only
+        return (f"{info.get('model name', 'unknown')} (family {info.get('cpu family', '?')}, "
+                f"model {info.get('model', '?')}, stepping {info.get('stepping', '?')})")
+    except OSError:
+        return "unknown"
 
 
 def _cpu_cores(torch):
