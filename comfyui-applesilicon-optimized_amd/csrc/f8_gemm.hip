@@ -17,7 +17,7 @@ int run_w8a16_tiled(const uint16_t* a, int64_t lda, const uint8_t* w, int64_t ld
   const Src2 sa{reinterpret_cast<const uint8_t*>(a), reinterpret_cast<const uint8_t*>(a), 2 * lda, M};
   const Src2 sb{w, w, ldw, N};
   return run_tiles<false>(M, N, N, K, sa, sb, w_scale, epi, s, what,
-                          [](auto) { return OpW8A16<BF16, HAS_SCALE>{}; });
+                          [](auto) { return OpW8A16<BF16, HAS_SCALE>{}; }, W8A16Tiles{});
 }
 
 }  // namespace

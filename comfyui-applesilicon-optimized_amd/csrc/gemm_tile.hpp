@@ -1523,12 +1523,20 @@ gemm_w4_kernel(GemmShape sh, Src2 sa, Src2 sb, const float* b_scale, Epi epi) {
 // the next one (last step); across tiles the ring already holds the next
 // tile's first stage. Each accumulator takes its K steps and K halves in
 // the order of gemm_pingpong_kernel, so the results are the same bits.
-template <bool BF16, bool HAS_SCALE, int WM, int WN, int NBUF, class Epi>
+//
+// BM_ = 224 (1 x 4 waves of 224 x 64, seven block rows) evens out the rounds
+// of GEMMs whose 256-row tiles leave most of a last round idle (9216 rows x
+// 3072 columns: 432 tiles of 256 x 256 on 256 CUs are 1.69 rounds, 504
+// tiles of 224 x 256 are 1.97); the schedule is the same with 14 slots per
+// block column and the four dequant words at slots 2, 5, 8 and 11 of a
+// column.
+template <bool BF16, bool HAS_SCALE, int WM, int WN, int NBUF, class Epi, int BM_ = 256>
 __global__ void __launch_bounds__(256)
 gemm_w4a16_kernel(GemmShape sh, Src2 sa, Src2 sb, const float* b_scale, Epi epi) {
   using Op = OpW8A16<BF16, HAS_SCALE>;
-  constexpr int BM = 256, BN = 256, NT = 256;
+  constexpr int BM = BM_, BN = 256, NT = 256;
   static_assert(WM * WN == 4, "four waves");
+  static_assert(BM % (32 * WM) == 0 && (BM == 256 || WM == 1), "whole block rows per wave");
   constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
   static_assert(TN >= 2 && TM >= 4, "the slot schedule needs two block columns and four rows");
   constexpr int SA = Op::SA, SB = Op::SB, S = Op::S;
@@ -1671,9 +1679,11 @@ gemm_w4a16_kernel(GemmShape sh, Src2 sa, Src2 sb, const float* b_scale, Epi epi)
           if constexpr (k == kCol)
             fq[TN - 1] = reinterpret_cast<lds_i32x4*>(pb)[(TN - 1) * 32 * SB / 16];
           // dequant: the last column of this step during column 0, column
-          // jb - 1 of the next step during column jb; one word per kCol / 4 slots
+          // jb - 1 of the next step during column jb; one word every kCol / 4
+          // slots (rounded down: words 0..3 at slots kW - 1, 2 kW - 1, ...)
           constexpr int kW = kCol / 4;
-          if constexpr (k % kW == kW - 1) {
+          static_assert(kW >= 1 && 4 * kW <= kCol, "four dequant words per column");
+          if constexpr ((k % kCol) % kW == kW - 1 && (k % kCol) / kW < 4) {
             constexpr int w = (k % kCol) / kW;
             if constexpr (jb == 0) Op::template dequant_word<w>(fq[TN - 1], ws, bq[TN - 1]);
             else Op::template dequant_word<w>(fq[jb - 1], ws, bq[jb - 1]);

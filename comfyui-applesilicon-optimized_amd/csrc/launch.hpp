@@ -130,6 +130,16 @@ inline int w4a16_mode() {
 template <class T, class Op, bool PAIR, class Epi>
 int launch_tile(const GemmShape& sh, const Src2& sa, const Src2& sb, const float* b_scale,
                 const Epi& epi, hipStream_t s, const char* what) {
+  // 224 x 256: the W8A16 one-wave-per-SIMD kernel only (W8A16Tiles)
+  if constexpr (T::BM == 224) {
+    static_assert(IsW8A16<Op>::value && !PAIR && T::BN == 256 && T::WM == 1 && T::WN == 4,
+                  "the 224-row tile is W8A16 on 1 x 4 waves");
+    auto kernel = gemm_w4a16_kernel<IsW8A16<Op>::kBF16, IsW8A16<Op>::kScale, 1, 4, 3, Epi, 224>;
+    static int bocc = 0;
+    const int grid = persistent_grid(kernel, 256, sh.count, bocc);
+    hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(256), 0, s, sh, sa, sb, b_scale, epi);
+    return check_launch(what);
+  } else {
   if constexpr (IsW8A16<Op>::value && !PAIR && T::BM == 256 && T::BN == 256 && T::WM == 2 &&
                 T::WN == 4 && T::KG == 1) {
     const int mode = w4a16_mode();
@@ -178,6 +188,7 @@ int launch_tile(const GemmShape& sh, const Src2& sa, const Src2& sb, const float
     const int grid = persistent_grid(kernel, T::NT, sh.count, occ);
     hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(T::NT), 0, s, sh, sa, sb, b_scale, epi);
     return check_launch(what);
+  }
   }
 }
 
@@ -272,6 +283,36 @@ struct MainTiles {
   static int bm(int id) { return tile_bm(id); }
   static int bn(int id) { return tile_bn(id); }
   static TilePlan plan(int64_t M, int64_t N, int64_t K, int cus) { return plan_tiles(M, N, K, cus); }
+};
+
+// The tile set of W8A16 GEMMs: the general set plus 224 x 256 (id
+// TILE_224x256_W8A16; gemm_w4a16_kernel with 1 x 4 waves of 224 x 64), which
+// the cost model takes where 256-row tiles would leave a last round mostly
+// idle. Its relative per-CU throughput, 0.92 of the 256 x 256 tile of the
+// same kernel, is measured on MI355X (same process, bits identical): two
+// full rounds of each at 9216 x 3072, K = 3072 and 12288, take 156.0 against
+// 162.9 us and 581.6 against 607.5 us for 7/8 the work per tile.
+// C4Q_TILE=0..8 forces one launch of one of them, for tuning sweeps.
+constexpr int TILE_224x256_W8A16 = TILE_COUNT;
+struct W8A16Tiles {
+  template <class F> static int with(int id, F&& f) {
+    if (id == TILE_224x256_W8A16) return f(Tile<224, 256, 1, 4, 160, 128>{});
+    return with_tile(id, f);
+  }
+  static int bm(int id) { return id == TILE_224x256_W8A16 ? 224 : tile_bm(id); }
+  static int bn(int id) { return id == TILE_224x256_W8A16 ? 256 : tile_bn(id); }
+  static TilePlan plan(int64_t M, int64_t N, int64_t K, int cus) {
+    const int id = forced_tile("C4Q_TILE", TILE_COUNT + 1);
+    if (id >= 0) return {id, cdiv(M, bm(id)) * cdiv(N, bn(id)), -1};
+    static const TileCand cands[] = {{TILE_256x256_W8, 1, 1.00},
+                                     {TILE_224x256_W8A16, 1, 0.92},
+                                     {TILE_128x128_W4_K128, 2, 0.87},
+                                     {TILE_64x128_W4_K128, 2, 0.70}};
+    static const TileCand tails[] = {{TILE_128x128_W4_K128, 2, 0.87},
+                                     {TILE_64x128_W4_K128, 2, 0.70},
+                                     {TILE_64x64_KG4, 1, 0.30}};
+    return plan_from(cands, 4, tails, 3, bm, bn, M, N, K, cus);
+  }
 };
 
 // Tiles whose waves each span 128 output columns -- one attention head --

@@ -1,9 +1,9 @@
 // Host-side checks of the library's own planning and error code under
 // AddressSanitizer and UndefinedBehaviorSanitizer (built host-only by
 // tests/native/Makefile, run on the CPU by tests/test_host_sanitized.py):
-//   * the tile plans of both tile sets (plan_launches, tile_at: the functions
+//   * the tile plans of the three tile sets (plan_launches, tile_at: the functions
 //     the entry points run before every launch) over a grid of shapes, K
-//     values and CU counts, each 64 x 64 output cell computed exactly once;
+//     values and CU counts, each 32 x 64 output cell computed exactly once;
 //   * the error path of the C ABI (set_error / c4q_last_error): formatting,
 //     truncation of over-long messages, the ABI version.
 // Exit status 0 when every check passes; a sanitizer report aborts.
@@ -33,11 +33,11 @@ void check_plan(int64_t M, int64_t N, int64_t K, int cus) {
   GemmShape shs[2];
   const int n = plan_launches<Set>(M, N, N, K, cus, ids, shs);
   if (n < 1 || n > 2) return fail("launch count", M, N, K, cus);
-  const int64_t cm = cdiv(M, 64), cn = cdiv(N, 64);
+  const int64_t cm = cdiv(M, 32), cn = cdiv(N, 64);     // cells of 32 rows x 64 columns
   std::vector<int> cover((size_t)(cm * cn), 0);
   for (int l = 0; l < n; ++l) {
     const int bm = Set::bm(ids[l]), bn = Set::bn(ids[l]);
-    if (bm <= 0 || bn <= 0 || bm % 64 || bn % 64) return fail("tile size", M, N, K, cus);
+    if (bm <= 0 || bn <= 0 || bm % 32 || bn % 64) return fail("tile size", M, N, K, cus);
     if (shs[l].count <= 0) return fail("empty launch", M, N, K, cus);
     // kernel tiles lie in the grid of mapped tiles (a leftover mapped tile
     // split into pieces can leave a piece wholly past the matrix edge: it
@@ -49,9 +49,9 @@ void check_plan(int64_t M, int64_t N, int64_t K, int cus) {
       if (t.tm < 0 || t.tn < 0 || t.tm >= tm_max || t.tn >= tn_max)
         return fail("tile outside the mapped grid", M, N, K, cus);
       if ((int64_t)t.tm * bm >= M || (int64_t)t.tn * bn >= N) ++idle_pieces;
-      for (int64_t r = (int64_t)t.tm * bm; r < (int64_t)(t.tm + 1) * bm && r < M; r += 64)
+      for (int64_t r = (int64_t)t.tm * bm; r < (int64_t)(t.tm + 1) * bm && r < M; r += 32)
         for (int64_t c = (int64_t)t.tn * bn; c < (int64_t)(t.tn + 1) * bn && c < N; c += 64)
-          ++cover[(size_t)((r / 64) * cn + c / 64)];
+          ++cover[(size_t)((r / 32) * cn + c / 64)];
     }
   }
   for (int v : cover)
@@ -84,7 +84,8 @@ int main() {
         for (int cus : cus_list) {
           check_plan<MainTiles>(M, N, K, cus);
           check_plan<HeadTiles>(M, N, K, cus);
-          plans += 2;
+          check_plan<W8A16Tiles>(M, N, K, cus);
+          plans += 3;
         }
   check_errors();
   printf("%d plans checked, %d failures (%lld leftover pieces wholly past the edge)\n", plans,

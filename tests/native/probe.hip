@@ -148,15 +148,15 @@ extern "C" int c4q_probe_e4m3_exhaustive(int which, unsigned long long* out, voi
 // ---------------------------------------------------------- tile plans ---
 // Host-side enumeration of the launches a GEMM's tile plan issues
 // (plan_launches, tile_at -- the functions the library runs). cover
-// [cdiv(M, 64) * cdiv(n_rows_b, 64)] counts, per 64 x 64 output cell
+// [cdiv(M, CM) * cdiv(n_rows_b, 64)] counts, per CM x 64 output cell
 // inside the matrix, the kernel tiles that compute it (every tile size is a
 // multiple of the cell). info[8]: launches, then (tile id, kernel tiles) of
 // each launch, then the main launch's first and the tail launch's sub_m,
 // sub_n. Returns 0, or -1 if cover_len is too small.
-template <class Set>
+template <class Set, int CM = 64>
 static int probe_plan(int64_t M, int64_t n_rows_b, int64_t K, int cus, int32_t* cover,
                       int64_t cover_len, int64_t* info) {
-  const int64_t cm = cdiv(M, 64), cn = cdiv(n_rows_b, 64);
+  const int64_t cm = cdiv(M, CM), cn = cdiv(n_rows_b, 64);
   if (cm * cn > cover_len) return -1;
   for (int64_t i = 0; i < cm * cn; ++i) cover[i] = 0;
   int ids[2];
@@ -174,9 +174,9 @@ static int probe_plan(int64_t M, int64_t n_rows_b, int64_t K, int cus, int32_t* 
     }
     for (int i = 0; i < shs[l].count; ++i) {
       const TileCoord t = tile_at(shs[l], i);
-      for (int64_t r = (int64_t)t.tm * bm; r < (int64_t)(t.tm + 1) * bm; r += 64)
+      for (int64_t r = (int64_t)t.tm * bm; r < (int64_t)(t.tm + 1) * bm; r += CM)
         for (int64_t c = (int64_t)t.tn * bn; c < (int64_t)(t.tn + 1) * bn; c += 64)
-          if (r < M && c < n_rows_b) ++cover[(r / 64) * cn + c / 64];
+          if (r < M && c < n_rows_b) ++cover[(r / CM) * cn + c / 64];
     }
   }
   info[5] = n ? shs[0].first : 0;
@@ -186,6 +186,14 @@ static int probe_plan(int64_t M, int64_t n_rows_b, int64_t K, int cus, int32_t* 
 extern "C" int c4q_probe_tile_plan(int64_t M, int64_t n_rows_b, int64_t K, int cus, int32_t* cover,
                                    int64_t cover_len, int64_t* info) {
   return probe_plan<MainTiles>(M, n_rows_b, K, cus, cover, cover_len, info);
+}
+
+// The same for the W8A16 tile set (W8A16Tiles: the general ids plus 8 =
+// 224x256 on 1 x 4 waves), over cells of 32 rows x 64 columns: cover has
+// cdiv(M, 32) * cdiv(n_rows_b, 64) entries.
+extern "C" int c4q_probe_w8a16_tile_plan(int64_t M, int64_t n_rows_b, int64_t K, int cus,
+                                         int32_t* cover, int64_t cover_len, int64_t* info) {
+  return probe_plan<W8A16Tiles, 32>(M, n_rows_b, K, cus, cover, cover_len, info);
 }
 
 // The same for the head-spanning tile set (HeadTiles: ids 0 = 256x256 with

@@ -963,6 +963,59 @@ def test_every_tile_variant(dev, monkeypatch, tile):
     assert_close(bf16_to_f32(bits16(y)), bf16_to_f32(ref), f"tile {tile} w8a16")
 
 
+# ------------------------------------------------- W8A16 224-row tile ---
+# W8A16 GEMMs may run on 224 x 256 tiles (seven 32-row blocks per wave of
+# the one-wave-per-SIMD kernel). Forced (C4Q_TILE=8) on ragged shapes, each
+# output is checked against the oracle and, bit for bit, against the same
+# GEMM on 256 x 256 tiles (C4Q_TILE=0): both accumulate every element's K
+# products in the same order.
+
+W8A16_224_CASES = [
+    # M, K, N, x dtype, scaled, bias dtype, out dtype, GELU table
+    (300, 1040, 520, torch.bfloat16, True, torch.bfloat16, None, False),    # ragged M, N, K tail
+    (449, 3072, 700, torch.bfloat16, True, torch.bfloat16, None, True),     # last tile: one row
+    (224, 3072, 3072, torch.bfloat16, False, torch.float32, None, False),   # one whole tile row
+    (1000, 16, 256, torch.float16, True, None, None, False),                # one K step
+    (672, 12288, 300, torch.bfloat16, True, torch.bfloat16, torch.float32, False),  # long K, f32 out
+    (2100, 3072, 3072, torch.float16, False, torch.float16, None, False),   # several rounds
+]
+
+
+@pytest.mark.parametrize("M,K,N,xdt,scaled,bias_dt,out_dt,gelu", W8A16_224_CASES)
+def test_w8a16_224_row_tile_exact(dev, monkeypatch, M, K, N, xdt, scaled, bias_dt, out_dt, gelu):
+    g = gen(224 + M + K + N)
+    x = torch.randn(M, K, generator=g).to(xdt)
+    wf = 0.02 * torch.randn(N, K, generator=g)
+    ws = wf.abs().amax() / 448 if scaled else None
+    w = _fp8(wf / ws) if scaled else _fp8(wf * 20)
+    bias = (0.01 * torch.randn(N, generator=g)).to(bias_dt) if bias_dt is not None else None
+    table = ops.act_table("gelu_tanh", dev) if gelu else None
+    xd_, wd_ = x.to(dev), w.to(dev)
+    sd_ = ws.reshape(1).to(dev) if scaled else None
+    bd_ = bias.to(dev) if bias is not None else None
+
+    def run(tile):
+        monkeypatch.setenv("C4Q_TILE", tile)
+        return ops.w8a16_linear(xd_, wd_, sd_, bd_, out_dtype=out_dt, act_table=table).cpu()
+
+    y224, y256 = run("8"), run("0")
+    assert y224.dtype == y256.dtype and y224.shape == (M, N)
+    assert torch.equal(y224.view(torch.int16) if y224.dtype != torch.float32 else y224.view(torch.int32),
+                       y256.view(torch.int16) if y256.dtype != torch.float32 else y256.view(torch.int32)), \
+        f"224-row tile != 256-row tile ({M}x{K}x{N})"
+    xd = "bf16" if xdt == torch.bfloat16 else "f16"
+    od = "f32" if out_dt == torch.float32 else xd
+    bd = {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "f32", None: "f32"}[bias_dt]
+    braw = None if bias is None else (bias.numpy() if bias_dt == torch.float32 else bits16(bias))
+    ref = of.w8a16_linear(bits16(x), u8(w), ws.numpy() if scaled else None, braw, bd, xd, od,
+                          act="gelu_tanh" if gelu else None)
+    if od == "f32":
+        assert_close(y224.numpy(), ref, f"w8a16 224-row tile {M}x{K}x{N} f32")
+        return
+    tof = bf16_bits_to_f32 if xd == "bf16" else f16_bits_to_f32
+    assert_close(tof(bits16(y224)), tof(ref), f"w8a16 224-row tile {M}x{K}x{N}")
+
+
 # ------------------------------------------------------ split tile plans ---
 # Shapes whose last round of 256x256 tiles would leave most CUs idle: the
 # library runs the whole rounds as one launch and splits the leftover tiles

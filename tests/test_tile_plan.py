@@ -171,3 +171,68 @@ def test_head_plan_h3_8192(head_probe):
     _, info = plan(head_probe, 8192, 21504, 5376, 256)
     assert info[0] == 2 and (info[1], info[2]) == (HEAD_256, 2560)
     assert (info[3], info[4]) == (HEAD_128, 512) and (info[6], info[7]) == (2, 2)
+
+
+# ------------------------------------------------------- W8A16 tile set ---
+# W8A16Tiles: the general ids plus 224x256 (one-wave-per-SIMD W8A16 kernel
+# with seven 32-row block rows per wave), which the cost model takes where
+# 256-row tiles would leave most of a last round idle. Coverage is counted
+# in cells of 32 rows x 64 columns.
+W8A16_224 = 8
+
+
+@pytest.fixture(scope="module")
+def w8a16_probe():
+    if not LIB.exists():
+        subprocess.run(["make", "-C", str(NATIVE)], check=True)
+    lib = ctypes.CDLL(str(LIB))
+    f = lib.c4q_probe_w8a16_tile_plan
+    f.argtypes = [ctypes.c_int64] * 3 + [ctypes.c_int, ctypes.c_void_p, ctypes.c_int64,
+                                         ctypes.c_void_p]
+    f.restype = ctypes.c_int
+    return f
+
+
+def plan32(probe, M, n_rows_b, K, cus):
+    cover = np.zeros(-(-M // 32) * -(-n_rows_b // 64), np.int32)
+    info = np.zeros(8, np.int64)
+    assert probe(M, n_rows_b, K, cus, cover.ctypes.data, cover.size, info.ctypes.data) == 0
+    return cover, info
+
+
+@pytest.mark.parametrize("cus", [256, 304, 80])
+@pytest.mark.parametrize("M,NB,K", SHAPES)
+def test_w8a16_plan_every_cell_once(w8a16_probe, M, NB, K, cus):
+    cover, info = plan32(w8a16_probe, M, NB, K, cus)
+    assert info[0] in (1, 2)
+    assert cover.min() == 1 and cover.max() == 1, (M, NB, K, cus, info.tolist())
+
+
+def test_w8a16_plan_random_shapes(w8a16_probe):
+    rng = np.random.default_rng(3)
+    for _ in range(300):
+        M = int(rng.integers(1, 12000))
+        NB = int(rng.integers(1, 12000))
+        K = int(rng.choice([16, 64, 512, 3072, 12288]))
+        cus = int(rng.choice([256, 304, 120, 8]))
+        cover, info = plan32(w8a16_probe, M, NB, K, cus)
+        assert cover.min() == 1 and cover.max() == 1, (M, NB, K, cus, info.tolist())
+        if info[1] == W8A16_224:
+            assert info[0] == 1, "the 224-row tile takes no tail launch"
+
+
+def test_w8a16_out_proj_takes_224_rows(w8a16_probe):
+    """C2 / C5 out-projection and C5 MLP-down (9216 x 3072): 432 tiles of
+    256x256 are 1.69 rounds on 256 CUs; 42 x 12 = 504 tiles of 224x256 are
+    1.97 rounds of 7/8 the work each."""
+    for K in (3072, 12288):
+        _, info = plan32(w8a16_probe, 9216, 3072, K, 256)
+        assert info[0] == 1 and (info[1], info[2]) == (W8A16_224, 42 * 12)
+
+
+def test_w8a16_qkv_keeps_256_rows(w8a16_probe):
+    """C2 QKV (9216 x 9216): five whole rounds of 256x256 plus 256 split-K
+    pieces cost less than six rounds of 224x256 (1512 tiles)."""
+    _, info = plan32(w8a16_probe, 9216, 9216, 3072, 256)
+    assert info[0] == 2 and (info[1], info[2]) == (TILE_256, 1280)
+    assert (info[3], info[4]) == (TILE_64x64_KG4, 256)
