@@ -83,11 +83,19 @@ int run_w8a16_skinny(const uint16_t* a, int64_t lda, const uint8_t* w, int64_t l
   // block per wave across 12 waves already cover the HBM latency; deeper
   // prefetch only pays where each block's arithmetic is short -- MI355X,
   // N = 18432 / 3072, K = 3072). The bias width is a template parameter.
+  // M in (16, 32]: two 16-row activation groups per wave (MG = 2), half as
+  // many blocks per barrier.
   const int64_t slots = (int64_t)device_cus();
   const bool deep = M <= 4 && cdiv(nblk, slots) >= 2;
   auto pick = [&](auto bias_bits, auto depth) {
     constexpr int BIAS = decltype(bias_bits)::value, D = decltype(depth)::value;
-    static int occ12 = 0, occ16 = 0;
+    static int occ12 = 0, occ16 = 0, occ12g = 0, occ16g = 0;
+    if (M > 16) {
+      if (nch <= 4 * 12)
+        return launch(w8a16_skinny_kernel<BF16, HAS_SCALE, 4, 12, 1, 3, BIAS, Epi, 2>, 4, occ12g);
+      return launch(w8a16_skinny_kernel<BF16, HAS_SCALE, 4, kSkinnyMaxWaves, 1, 2, BIAS, Epi, 2>, 4,
+                    occ16g);
+    }
     if (nch <= 4 * 12)
       return launch(w8a16_skinny_kernel<BF16, HAS_SCALE, 4, 12, D, 6, BIAS, Epi>, 4, occ12);
     return launch(w8a16_skinny_kernel<BF16, HAS_SCALE, 4, kSkinnyMaxWaves, D, 4, BIAS, Epi>, 4, occ16);

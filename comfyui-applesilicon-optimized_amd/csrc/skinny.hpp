@@ -29,6 +29,14 @@
 //     areas are double-buffered.
 // Weights are dequantized in registers exactly like the tiled kernel
 // (dequant4: decode, optional kitchen scale, round to the activation type).
+//
+// MG = 2 takes M <= 32 as two 16-row activation groups (the reference runs
+// a separate small-M pipeline up to M = 64,
+// _patches/fp8s_ext/w8a16_gemm.mm:215-220): each wave keeps both groups'
+// K-slices in registers, every dequantized weight chunk feeds the MFMAs of
+// both groups, and the partial tiles and the per-group sums double (half as
+// many blocks per barrier, so the partial-tile area stays the same size).
+// The weight stream, which bounds the kernel, is read once.
 #pragma once
 #include "gemm_tile.hpp"
 
@@ -58,7 +66,7 @@ __device__ __forceinline__ void unroll_steps(F& f, int64_t i0, int64_t nb) {
   }
 }
 
-constexpr int kSkinnyMaxM = 16;
+constexpr int kSkinnyMaxM = 32;      // 16-row activation groups: one, or two (MG = 2)
 constexpr int kSkinnyMaxWaves = 16;
 constexpr int kSkinnyMaxK = 64 * 4 * kSkinnyMaxWaves;  // 4 chunks per wave at most waves
 
@@ -89,13 +97,15 @@ __device__ __forceinline__ void mask_halves(i32x4& lo, i32x4& hi, int kb, int64_
 // workgroup per CU: MAXW / 4 waves per SIMD, so 512 / (MAXW / 4) VGPRs per
 // wave (16 waves: 128; 12 waves: 168).
 // BIAS: 0 none, 16 a bf16/f16 bias, 32 an f32 bias (Epi = EpiW8A16).
-template <bool BF16, bool HAS_SCALE, int CPW, int MAXW, int D, int P, int BIAS, class Epi>
+template <bool BF16, bool HAS_SCALE, int CPW, int MAXW, int D, int P, int BIAS, class Epi,
+          int MG = 1>
 __global__ void __launch_bounds__(64 * MAXW, MAXW / 4)
 w8a16_skinny_kernel(const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t ldw,
                     const float* w_scale, int64_t M, int64_t N, int64_t K, Epi epi) {
   static_assert(MAXW <= kSkinnyMaxWaves && MAXW % 4 == 0, "whole waves per SIMD");
   static_assert(D >= 1 && P >= 1, "pipeline shape");
-  __shared__ f32x4 red[2][P][MAXW][64];    // partial tiles of two groups of blocks
+  static_assert(MG == 1 || MG == 2, "one or two 16-row activation groups");
+  __shared__ f32x4 red[2][P][MG][MAXW][64];    // partial tiles of two groups of blocks
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
   const int r = lane & 15, g = lane >> 4;
   const int nch = (int)((K + 63) / 64);
@@ -137,28 +147,34 @@ w8a16_skinny_kernel(const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t ld
   // latencies overlap (D = 1: each step loads its own block).
   if constexpr (D >= 2) fetch(0, qb[0]);
 
-  // this wave's K-slice of activation row r, kept in registers
+  // this wave's K-slice of activation rows r (+ 16 per group), kept in
+  // registers
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(reinterpret_cast<const uint8_t*>(x), M * ldx * 2);
-  i32x4 xa[CPW], xb[CPW];
+  i32x4 xa[MG][CPW], xb[MG][CPW];
 #pragma unroll
-  for (int j = 0; j < CPW; ++j) {
-    const int c = wave * CPW + j;
-    const int kb = c * 64 + 16 * g;
-    const bool live = c < nch && r < M;
-    const int off = live ? (int)(r * ldx * 2) + 2 * kb : kOOB;
-    xa[j] = __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0);
-    xb[j] = __builtin_amdgcn_raw_buffer_load_b128(xr, live ? off + 16 : kOOB, 0, 0);
-  }
+  for (int mg = 0; mg < MG; ++mg)
+#pragma unroll
+    for (int j = 0; j < CPW; ++j) {
+      const int c = wave * CPW + j;
+      const int kb = c * 64 + 16 * g;
+      const int row = r + 16 * mg;
+      const bool live = c < nch && row < M;
+      const int off = live ? (int)(row * ldx * 2) + 2 * kb : kOOB;
+      xa[mg][j] = __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0);
+      xb[mg][j] = __builtin_amdgcn_raw_buffer_load_b128(xr, live ? off + 16 : kOOB, 0, 0);
+    }
   // K tail: only a wave whose slice runs past K masks (a wave-uniform test --
   // a per-lane one would make every wave wait here for its activation
   // loads, and behind them for the first block's weights, before the rest
   // of the prologue prefetch goes out)
   if ((wave + 1) * CPW * 64 > K) {
 #pragma unroll
-    for (int j = 0; j < CPW; ++j) {
-      const int kb = (wave * CPW + j) * 64 + 16 * g;
-      if (kb + 16 > K) mask_halves(xa[j], xb[j], kb, K);
-    }
+    for (int mg = 0; mg < MG; ++mg)
+#pragma unroll
+      for (int j = 0; j < CPW; ++j) {
+        const int kb = (wave * CPW + j) * 64 + 16 * g;
+        if (kb + 16 > K) mask_halves(xa[mg][j], xb[mg][j], kb, K);
+      }
   }
 #pragma unroll
   for (int p = 1; p < D - 1; ++p) fetch(p, qb[p]);
@@ -166,7 +182,9 @@ w8a16_skinny_kernel(const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t ld
   // Multiply one block and publish the wave's partial tile (row-major,
   // m = 4*(lane/16) + i, c = lane%16) -- no barrier per block.
   auto run_block = [&](i32x4 (&q)[CPW], int buf, int slot) {
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    f32x4 acc[MG];
+#pragma unroll
+    for (int mg = 0; mg < MG; ++mg) acc[mg] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < CPW; ++j) {
       const int c = wave * CPW + j;
@@ -180,14 +198,20 @@ w8a16_skinny_kernel(const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t ld
       dequant4<BF16, HAS_SCALE>((uint32_t)q[j].w, ws, o[6], o[7]);
       const i32x4 b0 = {(int)o[0], (int)o[1], (int)o[2], (int)o[3]};
       const i32x4 b1 = {(int)o[4], (int)o[5], (int)o[6], (int)o[7]};
-      acc = mfma16<BF16>(xa[j], b0, acc);
-      acc = mfma16<BF16>(xb[j], b1, acc);
+#pragma unroll
+      for (int mg = 0; mg < MG; ++mg) {
+        acc[mg] = mfma16<BF16>(xa[mg][j], b0, acc[mg]);
+        acc[mg] = mfma16<BF16>(xb[mg][j], b1, acc[mg]);
+      }
     }
-    float* t = reinterpret_cast<float*>(&red[buf][slot][wave][0]);
-    t[(4 * g + 0) * 16 + r] = acc.x;
-    t[(4 * g + 1) * 16 + r] = acc.y;
-    t[(4 * g + 2) * 16 + r] = acc.z;
-    t[(4 * g + 3) * 16 + r] = acc.w;
+#pragma unroll
+    for (int mg = 0; mg < MG; ++mg) {
+      float* t = reinterpret_cast<float*>(&red[buf][slot][mg][wave][0]);
+      t[(4 * g + 0) * 16 + r] = acc[mg].x;
+      t[(4 * g + 1) * 16 + r] = acc[mg].y;
+      t[(4 * g + 2) * 16 + r] = acc[mg].z;
+      t[(4 * g + 3) * 16 + r] = acc[mg].w;
+    }
   };
   // Bias of this thread's four columns of block blk. The block's 16
   // bias values are wave-uniform (a wave stores the pieces of one block), so
@@ -230,19 +254,23 @@ w8a16_skinny_kernel(const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t ld
     const int64_t i = gi * pg + pslot;
     if (pslot >= pg || i >= nb) return;                 // wave-uniform
     const typename Epi::Col col = block_col((int64_t)blockIdx.x + i * G);
-    if (em >= M) return;
     const int64_t n = ((int64_t)blockIdx.x + i * G) * 16 + ecq;
     if (n >= N) return;
     const int idx = em * 4 + (ecq >> 2);
-    f32x4 sum = red[buf][pslot][0][idx];
-#pragma unroll
-    for (int wv = 1; wv < MAXW; ++wv) {
-      if (wv < nwaves) sum += red[buf][pslot][wv][idx];
-      if ((wv & 3) == 3) __builtin_amdgcn_sched_barrier(0);   // four tiles in flight at most
-    }
-    const float v[4] = {sum.x, sum.y, sum.z, sum.w};
     const int nv = N - n < 4 ? (int)(N - n) : 4;
-    store_group(ep, em, n, nv, ep.apply(ep.rowp(em), col, v));
+#pragma unroll
+    for (int mg = 0; mg < MG; ++mg) {
+      const int row = em + 16 * mg;
+      if (row >= M) break;
+      f32x4 sum = red[buf][pslot][mg][0][idx];
+#pragma unroll
+      for (int wv = 1; wv < MAXW; ++wv) {
+        if (wv < nwaves) sum += red[buf][pslot][mg][wv][idx];
+        if ((wv & 3) == 3) __builtin_amdgcn_sched_barrier(0);   // four tiles in flight at most
+      }
+      const float v[4] = {sum.x, sum.y, sum.z, sum.w};
+      store_group(ep, row, n, nv, ep.apply(ep.rowp(row), col, v));
+    }
   };
 
   // Step i (weight buffer B = i % D, group gi = i / pg, slot i % pg): issue

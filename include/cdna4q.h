@@ -245,7 +245,7 @@ int c4q_fp8_dequant(const uint8_t* w, int64_t n, const float* scale, void* out,
  * activation type, W' = T(decode(W) * T(w_scale[0])) (w_scale NULL = plain
  * decode). act_table (bf16 output only, or NULL): 65,536 bf16 entries applied
  * to the rounded output (e.g. GELU-tanh for an MLP up-projection).
- * M <= 16 (decode shapes, K <= 4096, aligned operands) takes a split-K route
+ * M <= 32 (decode shapes, K <= 4096, aligned operands) takes a split-K route
  * that streams W at memory bandwidth; larger M the MFMA-tiled route.
  * Replaces w8a16_bias_bf16 / w8a16_f32
  * (_patches/fp8s_ext/w8a16_gemm.mm:286-314) behind _w8a16_forward

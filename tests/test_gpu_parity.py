@@ -818,7 +818,13 @@ def test_w8a16_dequant_exact_every_code(dev, xdt, scale, M):
     (3, 24, 40, torch.bfloat16, True, torch.bfloat16, None),         # K < one chunk
     (7, 4160, 300, torch.float16, True, torch.float32, None),        # f16 activations
     (5, 3072, 260, torch.bfloat16, True, torch.bfloat16, torch.float32),
-    (17, 3072, 512, torch.bfloat16, True, torch.bfloat16, None),     # first M past the small-M route
+    (17, 3072, 512, torch.bfloat16, True, torch.bfloat16, None),     # two row groups, one row in the second
+    (32, 3072, 3072, torch.bfloat16, True, torch.bfloat16, None),    # two full row groups
+    (24, 3072, 18432, torch.bfloat16, True, torch.float32, None),    # two groups, several blocks per workgroup
+    (32, 4096, 20000, torch.bfloat16, True, torch.bfloat16, None),   # two groups on the 16-wave variant
+    (29, 1040, 17, torch.float16, False, torch.float16, None),       # two groups, K tail, f16, ragged N
+    (20, 3000, 33333, torch.bfloat16, True, None, torch.float32),    # two groups, ragged K, f32 out
+    (33, 3072, 512, torch.bfloat16, True, torch.bfloat16, None),     # first M past the small-M route
     (2, 4096, 96, torch.bfloat16, True, torch.bfloat16, None),       # largest K of the small-M route
     (2, 4112, 96, torch.bfloat16, True, torch.bfloat16, None),       # K past it: tiled route
     (16, 3072, 18432, torch.bfloat16, True, torch.bfloat16, None),   # several blocks per workgroup
@@ -838,8 +844,8 @@ def test_w8a16_small_m(dev, M, K, N, xdt, scaled, bias_dt, out_dt):
     out = ops.w8a16_linear(x.to(dev), w.to(dev), ws.reshape(1).to(dev) if scaled else None,
                            bias.to(dev) if bias is not None else None, out_dtype=out_dt)
     xd = "bf16" if xdt == torch.bfloat16 else "f16"
-    bd = {torch.bfloat16: "bf16", torch.float32: "f32", None: "f32"}[bias_dt]
-    braw = None if bias is None else (bits16(bias) if bias_dt == torch.bfloat16 else bias.numpy())
+    bd = {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "f32", None: "f32"}[bias_dt]
+    braw = None if bias is None else (bias.numpy() if bias_dt == torch.float32 else bits16(bias))
     od = "f32" if out_dt == torch.float32 else xd
     ref = of.w8a16_linear(bits16(x), u8(w), ws.numpy() if scaled else None, braw, bd, xd, od)
     if od == "f32":
@@ -849,10 +855,11 @@ def test_w8a16_small_m(dev, M, K, N, xdt, scaled, bias_dt, out_dt):
         assert_close(tof(bits16(out)), tof(ref), f"w8a16 small-M {M}x{K}x{N}")
 
 
-def test_w8a16_small_m_gelu_table(dev):
+@pytest.mark.parametrize("M", [4, 27])    # one and two 16-row activation groups
+def test_w8a16_small_m_gelu_table(dev, M):
     """Activation table on the small-M route: exact lookup of its own bf16 linear output."""
     g = gen(11)
-    M, K, N = 4, 3072, 1000
+    K, N = 3072, 1000
     x = torch.randn(M, K, generator=g).to(torch.bfloat16)
     wf = 0.02 * torch.randn(N, K, generator=g)
     ws = (wf.abs().amax() / 448).reshape(1)
