@@ -109,6 +109,17 @@ int run_w8a16_skinny(const uint16_t* a, int64_t lda, const uint8_t* w, int64_t l
   return with_depth(std::integral_constant<int, 16>{});
 }
 
+// M in (32, 64] with N up to this many columns runs as two passes of the
+// small-M kernel over the two row halves: the weights stream twice (the
+// second time mostly from the Infinity Cache), which beats the few tiles
+// the tiled route has for such M. Measured on MI355X, K = 3072, graph
+// replays with weights rotated past the Infinity Cache, against the tiled
+// route: N = 3072 1.42-1.77x, 6144 1.19-1.48x, 9216 1.01-1.29x, 12288
+// 1.00-1.21x, 18432 0.80-0.96x (M = 64 ... 33).
+constexpr int64_t kSkinnyTwoPassMaxN = 12288;
+
+// EpiW8A16 has no row parameters, so a row range of the output is the same
+// functor over an offset output pointer.
 template <class Epi>
 int run_w8a16(const void* a, int a_dtype, int64_t lda, const uint8_t* w, int64_t ldw,
               const float* w_scale, int64_t M, int64_t N, int64_t K, const Epi& epi, hipStream_t s,
@@ -118,25 +129,35 @@ int run_w8a16(const void* a, int a_dtype, int64_t lda, const uint8_t* w, int64_t
   // rows with 32-bit buffer offsets.
   // (the small-M kernel reads the bias through the scalar cache: a 4-byte
   // aligned base)
-  const bool skinny = M <= kSkinnyMaxM && K > 0 && K <= kSkinnyMaxK && aligned16(a) &&
-                      (epi.bias == nullptr || ((uintptr_t)epi.bias & 3) == 0) &&
-                      aligned16(w) && lda % 8 == 0 && ldw % 16 == 0 && 16 * ldw + 64 < (1ll << 31) &&
-                      kSkinnyMaxM * 2 * lda + 256 < (1ll << 31);
-  if (skinny) {
-    const uint16_t* a16 = static_cast<const uint16_t*>(a);
+  const bool skinny_ok = K > 0 && K <= kSkinnyMaxK && aligned16(a) &&
+                         (epi.bias == nullptr || ((uintptr_t)epi.bias & 3) == 0) &&
+                         aligned16(w) && lda % 8 == 0 && ldw % 16 == 0 &&
+                         16 * ldw + 64 < (1ll << 31) && kSkinnyMaxM * 2 * lda + 256 < (1ll << 31);
+  auto skinny = [&](const uint16_t* a16, int64_t m, const Epi& e) {
     if (bf16)
-      return w_scale ? run_w8a16_skinny<true, true>(a16, lda, w, ldw, w_scale, M, N, K, epi, s, what)
-                     : run_w8a16_skinny<true, false>(a16, lda, w, ldw, w_scale, M, N, K, epi, s, what);
-    return w_scale ? run_w8a16_skinny<false, true>(a16, lda, w, ldw, w_scale, M, N, K, epi, s, what)
-                   : run_w8a16_skinny<false, false>(a16, lda, w, ldw, w_scale, M, N, K, epi, s, what);
+      return w_scale ? run_w8a16_skinny<true, true>(a16, lda, w, ldw, w_scale, m, N, K, e, s, what)
+                     : run_w8a16_skinny<true, false>(a16, lda, w, ldw, w_scale, m, N, K, e, s, what);
+    return w_scale ? run_w8a16_skinny<false, true>(a16, lda, w, ldw, w_scale, m, N, K, e, s, what)
+                   : run_w8a16_skinny<false, false>(a16, lda, w, ldw, w_scale, m, N, K, e, s, what);
+  };
+  const uint16_t* a16 = static_cast<const uint16_t*>(a);
+  if (skinny_ok && M <= kSkinnyMaxM) return skinny(a16, M, epi);
+  if (skinny_ok && M <= 2 * kSkinnyMaxM && N <= kSkinnyTwoPassMaxN) {
+    const int64_t h = M / 2;                      // both halves within kSkinnyMaxM rows
+    using OutT = typename Epi::OutT;
+    Epi hi = epi;
+    hi.d = static_cast<uint8_t*>(epi.d) + h * epi.ldd * (int64_t)sizeof(OutT);
+    hi.vec = rows_vec16(hi.d, epi.ldd, sizeof(OutT));
+    const int st = skinny(a16, h, epi);
+    if (st != C4Q_OK) return st;
+    return skinny(a16 + h * lda, M - h, hi);
   }
   const bool tiled = K > 0 && K % 16 == 0 && aligned16(a) && aligned16(w) && lda % 8 == 0 &&
                      ldw % 16 == 0 && tile_offsets_fit(2 * lda, ldw);
   if (!tiled) {
-    GenW8A16 op{static_cast<const uint16_t*>(a), lda, w, ldw, w_scale, bf16 ? 1 : 0, 1.0f};
+    GenW8A16 op{a16, lda, w, ldw, w_scale, bf16 ? 1 : 0, 1.0f};
     return launch_generic(M, N, K, op, epi, s, what);
   }
-  const uint16_t* a16 = static_cast<const uint16_t*>(a);
   if (bf16) {
     return w_scale ? run_w8a16_tiled<true, true>(a16, lda, w, ldw, w_scale, M, N, K, epi, s, what)
                    : run_w8a16_tiled<true, false>(a16, lda, w, ldw, w_scale, M, N, K, epi, s, what);

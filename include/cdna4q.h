@@ -246,7 +246,8 @@ int c4q_fp8_dequant(const uint8_t* w, int64_t n, const float* scale, void* out,
  * decode). act_table (bf16 output only, or NULL): 65,536 bf16 entries applied
  * to the rounded output (e.g. GELU-tanh for an MLP up-projection).
  * M <= 32 (decode shapes, K <= 4096, aligned operands) takes a split-K route
- * that streams W at memory bandwidth; larger M the MFMA-tiled route.
+ * that streams W at memory bandwidth, M <= 64 with N <= 12288 two passes of
+ * it over the row halves; larger M the MFMA-tiled route.
  * Replaces w8a16_bias_bf16 / w8a16_f32
  * (_patches/fp8s_ext/w8a16_gemm.mm:286-314) behind _w8a16_forward
  * (_patches/linear_fp8_w8a16.py:151-196). */

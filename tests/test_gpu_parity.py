@@ -824,7 +824,12 @@ def test_w8a16_dequant_exact_every_code(dev, xdt, scale, M):
     (32, 4096, 20000, torch.bfloat16, True, torch.bfloat16, None),   # two groups on the 16-wave variant
     (29, 1040, 17, torch.float16, False, torch.float16, None),       # two groups, K tail, f16, ragged N
     (20, 3000, 33333, torch.bfloat16, True, None, torch.float32),    # two groups, ragged K, f32 out
-    (33, 3072, 512, torch.bfloat16, True, torch.bfloat16, None),     # first M past the small-M route
+    (33, 3072, 512, torch.bfloat16, True, torch.bfloat16, None),     # two passes: 16 + 17 rows
+    (48, 3072, 6000, torch.bfloat16, True, torch.float32, None),     # two passes of two groups
+    (64, 1040, 17, torch.float16, False, torch.float16, None),       # two passes, K tail, f16
+    (57, 3000, 12288, torch.bfloat16, True, None, torch.float32),    # two passes at the largest N, f32 out
+    (40, 3072, 12289, torch.bfloat16, True, torch.bfloat16, None),   # N past the two-pass route: tiled
+    (65, 3072, 512, torch.bfloat16, True, torch.bfloat16, None),     # first M past the small-M route
     (2, 4096, 96, torch.bfloat16, True, torch.bfloat16, None),       # largest K of the small-M route
     (2, 4112, 96, torch.bfloat16, True, torch.bfloat16, None),       # K past it: tiled route
     (16, 3072, 18432, torch.bfloat16, True, torch.bfloat16, None),   # several blocks per workgroup
@@ -855,7 +860,35 @@ def test_w8a16_small_m(dev, M, K, N, xdt, scaled, bias_dt, out_dt):
         assert_close(tof(bits16(out)), tof(ref), f"w8a16 small-M {M}x{K}x{N}")
 
 
-@pytest.mark.parametrize("M", [4, 27])    # one and two 16-row activation groups
+@pytest.mark.parametrize("M", [20, 50])    # one pass of two groups; two passes over the row halves
+def test_w8a16_small_m_strided_output(dev, M):
+    """Small-M route through the C ABI with padded activation and output rows
+    (lda = K + 24, ldd = N + 8): the result equals the contiguous call's, and
+    the padding columns keep their sentinel (the second pass of M > 32 writes
+    its rows at M // 2 of the strided output)."""
+    from cdna4q import _lib
+    g = gen(31 + M)
+    K, N = 3072, 1000
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    wf = 0.02 * torch.randn(N, K, generator=g)
+    ws = (wf.abs().amax() / 448).reshape(1)
+    w = _fp8(wf / ws)
+    bias = (0.01 * torch.randn(N, generator=g)).to(torch.bfloat16)
+    xd, wd, sd, bd = x.to(dev), w.to(dev), ws.to(dev), bias.to(dev)
+    ref = ops.w8a16_linear(xd, wd, sd, bd)
+    xp = torch.zeros(M, K + 24, dtype=torch.bfloat16, device=dev)
+    xp[:, :K] = xd
+    out = torch.full((M, N + 8), -7.0, dtype=torch.bfloat16, device=dev)
+    torch.cuda.synchronize()
+    _lib.call("c4q_w8a16_gemm_nt", xp.data_ptr(), 0, K + 24, wd.view(torch.uint8).data_ptr(), K,
+              sd.data_ptr(), out.data_ptr(), 0, N + 8, bd.data_ptr(), 0, None, M, N, K,
+              torch.cuda.current_stream(dev).cuda_stream)
+    torch.cuda.synchronize()
+    assert_bits_equal(bits16(out[:, :N].contiguous()), bits16(ref), f"strided small-M M={M}")
+    assert (out[:, N:].float() == -7.0).all(), "padding columns written"
+
+
+@pytest.mark.parametrize("M", [4, 27, 50])    # one and two 16-row activation groups; two passes
 def test_w8a16_small_m_gelu_table(dev, M):
     """Activation table on the small-M route: exact lookup of its own bf16 linear output."""
     g = gen(11)
