@@ -292,6 +292,12 @@ struct MainTiles {
 // same kernel, is measured on MI355X (same process, bits identical): two
 // full rounds of each at 9216 x 3072, K = 3072 and 12288, take 156.0 against
 // 162.9 us and 581.6 against 607.5 us for 7/8 the work per tile.
+// The split-K 64x64 tile is also a main candidate here (K >= 1024): with
+// few tiles each CU runs one long K chain, and W8A16's in-register dequant
+// makes that chain the bound; four wave groups over K cut it. Measured on
+// MI355X (K = 3072, against the 64x128 plan): M = 65-256, N = 3072
+// 32.9-33.2 -> 21.3-21.5 us; M = 128, K = 12288: 111.4 -> 46.6 us; where its
+// pieces need two or more rounds the cost model keeps the larger tiles.
 // C4Q_TILE=0..8 forces one launch of one of them, for tuning sweeps.
 constexpr int TILE_224x256_W8A16 = TILE_COUNT;
 struct W8A16Tiles {
@@ -307,11 +313,12 @@ struct W8A16Tiles {
     static const TileCand cands[] = {{TILE_256x256_W8, 1, 1.00},
                                      {TILE_224x256_W8A16, 1, 0.92},
                                      {TILE_128x128_W4_K128, 2, 0.87},
-                                     {TILE_64x128_W4_K128, 2, 0.70}};
+                                     {TILE_64x128_W4_K128, 2, 0.70},
+                                     {TILE_64x64_KG4, 1, 0.30}};
     static const TileCand tails[] = {{TILE_128x128_W4_K128, 2, 0.87},
                                      {TILE_64x128_W4_K128, 2, 0.70},
                                      {TILE_64x64_KG4, 1, 0.30}};
-    return plan_from(cands, 4, tails, 3, bm, bn, M, N, K, cus);
+    return plan_from(cands, K >= 1024 ? 5 : 4, tails, 3, bm, bn, M, N, K, cus);
   }
 };
 

@@ -860,6 +860,29 @@ def test_w8a16_small_m(dev, M, K, N, xdt, scaled, bias_dt, out_dt):
         assert_close(tof(bits16(out)), tof(ref), f"w8a16 small-M {M}x{K}x{N}")
 
 
+@pytest.mark.parametrize("M,K,N", [(128, 3072, 3072), (200, 3072, 1000), (65, 12288, 3072),
+                                   (130, 1040, 2000)])
+def test_w8a16_few_tiles_split_k_main(dev, monkeypatch, M, K, N):
+    """Few-tile W8A16 GEMMs whose plan runs the split-K 64x64 tile as the main
+    launch: against the oracle, and against the 64x128 tile (C4Q_TILE=5)
+    within one bf16 ulp plus the fp32 reordering (the K groups sum in another
+    order)."""
+    info = _w8a16_plan(M, N, K)
+    assert info[0] == 1 and info[1] == TILE_SPLIT_K, info.tolist()
+    g = gen(3 * M + K + N)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    wf = 0.02 * torch.randn(N, K, generator=g)
+    ws = (wf.abs().amax() / 448).reshape(1)
+    w = _fp8(wf / ws)
+    bias = (0.01 * torch.randn(N, generator=g)).to(torch.bfloat16)
+    args = (x.to(dev), w.to(dev), ws.to(dev), bias.to(dev))
+    y = bits16(ops.w8a16_linear(*args))
+    ref = of.w8a16_linear(bits16(x), u8(w), ws.numpy(), bits16(bias))
+    assert_close(bf16_to_f32(y), bf16_to_f32(ref), f"w8a16 split-K main {M}x{K}x{N}")
+    monkeypatch.setenv("C4Q_TILE", "5")
+    assert_reordered_sum_close(y, bits16(ops.w8a16_linear(*args)), "split-K main vs 64x128")
+
+
 @pytest.mark.parametrize("M", [20, 50])    # one pass of two groups; two passes over the row halves
 def test_w8a16_small_m_strided_output(dev, M):
     """Small-M route through the C ABI with padded activation and output rows
@@ -1082,6 +1105,20 @@ def _device_plan(M, n_rows_b, K):
 TILE_SPLIT_K = 7   # 64x64 pieces, K split over 4 wave groups
 
 
+def _w8a16_plan(M, N, K):
+    """The W8A16 tile set's plan on this device (info as in _device_plan)."""
+    import ctypes, pathlib
+    lib = ctypes.CDLL(str(pathlib.Path(__file__).resolve().parent / "native" / "libc4q_probe.so"))
+    f = lib.c4q_probe_w8a16_tile_plan
+    f.argtypes = [ctypes.c_int64] * 3 + [ctypes.c_int, ctypes.c_void_p, ctypes.c_int64,
+                                         ctypes.c_void_p]
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    cover = np.zeros(-(-M // 32) * -(-N // 64), np.int32)
+    info = np.zeros(8, np.int64)
+    assert f(M, N, K, cus, cover.ctypes.data, cover.size, info.ctypes.data) == 0
+    return info
+
+
 def assert_reordered_sum_close(out, ref, what):
     """bf16 results of the same products summed in another fp32 order: equal
     up to the final rounding (one bf16 ulp, 2^-7 relative) plus the fp32
@@ -1158,13 +1195,16 @@ def test_split_plan_fp8_and_w8a16(dev, monkeypatch, M, K, N):
                  f"split fp8 {M}x{K}x{N}")
     assert_close(bf16_to_f32(y), bf16_to_f32(of.w8a16_linear(bits16(x), u8(wf), ws.numpy(), bits16(bb))),
                  f"split w8a16 {M}x{K}x{N}")
+    wi = _w8a16_plan(M, N, K)            # W8A16 plans over its own tile set
     monkeypatch.setenv("C4Q_TILE", "0")
     o1, y1 = run()
     if info[3] == TILE_SPLIT_K:
         assert_reordered_sum_close(o, o1, "split-K fp8 vs one launch")
-        assert_reordered_sum_close(y, y1, "split-K w8a16 vs one launch")
     else:
         assert_bits_equal(o, o1, "split fp8 vs one launch")
+    if TILE_SPLIT_K in (wi[1], wi[3] if wi[0] == 2 else -1):
+        assert_reordered_sum_close(y, y1, "split-K w8a16 vs one launch")
+    else:
         assert_bits_equal(y, y1, "split w8a16 vs one launch")
 
 

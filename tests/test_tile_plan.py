@@ -236,3 +236,17 @@ def test_w8a16_qkv_keeps_256_rows(w8a16_probe):
     _, info = plan32(w8a16_probe, 9216, 9216, 3072, 256)
     assert info[0] == 2 and (info[1], info[2]) == (TILE_256, 1280)
     assert (info[3], info[4]) == (TILE_64x64_KG4, 256)
+
+
+def test_w8a16_few_tiles_take_split_k(w8a16_probe):
+    """Few-tile W8A16 GEMMs (one round of 64x64 split-K pieces covers them)
+    run on the split-K tile as the main launch when K >= 1024: M = 128,
+    N = 3072 is 96 pieces; with K = 512 the 64x128 tile stays."""
+    for M, N in ((65, 3072), (128, 3072), (256, 3072)):
+        cover, info = plan32(w8a16_probe, M, N, 3072, 256)
+        assert info[0] == 1 and info[1] == TILE_64x64_KG4, (M, N, info.tolist())
+        assert cover.min() == 1 and cover.max() == 1
+    _, info = plan32(w8a16_probe, 128, 3072, 512, 256)
+    assert info[1] != TILE_64x64_KG4
+    _, info = plan32(w8a16_probe, 1024, 3072, 3072, 256)     # 768 pieces: three rounds
+    assert info[1] != TILE_64x64_KG4
