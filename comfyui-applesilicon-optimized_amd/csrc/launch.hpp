@@ -318,7 +318,15 @@ struct W8A16Tiles {
     static const TileCand tails[] = {{TILE_128x128_W4_K128, 2, 0.87},
                                      {TILE_64x128_W4_K128, 2, 0.70},
                                      {TILE_64x64_KG4, 1, 0.30}};
-    return plan_from(cands, K >= 1024 ? 5 : 4, tails, 3, bm, bn, M, N, K, cus);
+    TilePlan p = plan_from(cands, K >= 1024 ? 5 : 4, tails, 3, bm, bn, M, N, K, cus);
+    // The model prices every round at two workgroups per CU. A 64x128 plan
+    // with more tiles than CUs whose 128x128 tiles fit one per CU runs
+    // faster on those (MI355X, K = 3072: 1024 x 3072 47.5 -> 43.2 us,
+    // 256 x 9216 47.6 -> 43.0 us, 128 x 18432 47.7 -> 44.4 us).
+    const int64_t t64 = cdiv(M, 64) * cdiv(N, 128), t128 = cdiv(M, 128) * cdiv(N, 128);
+    if (p.main_id == TILE_64x128_W4_K128 && p.tail_id < 0 && t64 > cus && t128 <= cus)
+      p = {TILE_128x128_W4_K128, t128, -1};
+    return p;
   }
 };
 

@@ -250,3 +250,15 @@ def test_w8a16_few_tiles_take_split_k(w8a16_probe):
     assert info[1] != TILE_64x64_KG4
     _, info = plan32(w8a16_probe, 1024, 3072, 3072, 256)     # 768 pieces: three rounds
     assert info[1] != TILE_64x64_KG4
+
+
+def test_w8a16_one_128_tile_per_cu(w8a16_probe):
+    """A 64x128 plan with more tiles than CUs whose 128x128 tiles fit one per
+    CU takes the 128x128 tile; 512 x 3072 (192 tiles of 64x128) keeps
+    64x128."""
+    for M, N in ((1024, 3072), (256, 9216), (128, 18432)):
+        cover, info = plan32(w8a16_probe, M, N, 3072, 256)
+        assert info[0] == 1 and info[1] == TILE_128_K128, (M, N, info.tolist())
+        assert cover.min() == 1 and cover.max() == 1
+    _, info = plan32(w8a16_probe, 512, 3072, 3072, 256)
+    assert info[1] == TILE_64x128_K128
